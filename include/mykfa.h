@@ -1,0 +1,198 @@
+/*
+ * mykfa — MI355X (gfx950) FlashAttention, C ABI.
+ *
+ * This library is the native side of the drop-in replacement for the Triton kernels in
+ * myk-llm's src/myk_llm/ops/flash_attn.py. Every entry point takes plain C structs of
+ * device pointers, element strides and ints, launches asynchronously on the caller's
+ * stream, never allocates or frees device memory, never synchronizes, and never throws or
+ * aborts across the ABI: it returns a status code and leaves a message readable through
+ * mykfa_last_error() on the calling thread.
+ *
+ * Semantics shared by every entry point (reference: flash_attn.py:11-22):
+ *   - queries are aligned to the END of the keys: query i of a sequence with Lq queries and
+ *     Lk keys sits at key position i + Lk - Lq and sees keys j with
+ *         i + Lk - Lq - window_left  <=  j  <=  i + Lk - Lq + window_right,   0 <= j < Lk;
+ *     a window side given as MYKFA_UNBOUNDED (2^30) is unbounded; causal is window_right=0
+ *     (reference: _window, flash_attn.py:435-439);
+ *   - GQA: query head h reads key/value head h / (num_heads / num_kv_heads)
+ *     (flash_attn.py:122);
+ *   - lse is the base-2 log-sum-exp of the scaled scores, fp32, laid out (num_heads, rows)
+ *     with rows = total packed tokens (varlen) or batch * seqlen_q (dense); a row that sees
+ *     no key gets lse = +inf and an output of 0 (flash_attn.py:147-153);
+ *   - strides are in ELEMENTS, as (batch, token, head); the last dimension must be
+ *     contiguous; batch stride 0 for packed varlen tensors (flash_attn.py:331-333).
+ */
+#ifndef MYKFA_H
+#define MYKFA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MYKFA_ABI_VERSION 1
+#define MYKFA_UNBOUNDED (1 << 30) /* flash_attn.py:32 (_UNBOUNDED) */
+
+/* Status codes. */
+#define MYKFA_OK 0
+#define MYKFA_ERR_INVALID 1     /* malformed arguments (null pointer, bad stride, shape) */
+#define MYKFA_ERR_UNSUPPORTED 2 /* valid but not implemented (head_dim, dtype) */
+#define MYKFA_ERR_LAUNCH 3      /* the HIP runtime rejected a launch */
+#define MYKFA_ERR_WORKSPACE 4   /* caller-provided workspace too small */
+
+/* Element types of q/k/v/o (reference accepts bf16 and fp16: flash_attn.py:340-341). */
+#define MYKFA_BF16 0
+#define MYKFA_FP16 1
+
+/* hipStream_t, without requiring the HIP headers in FFI users. NULL = default stream. */
+typedef struct ihipStream_t* mykfa_stream_t;
+
+/*
+ * Forward parameters. Replaces the argument list of _forward / _fwd_kernel
+ * (flash_attn.py:353-373, :106-114).
+ *   dense  : cu_seqlens_q == cu_seqlens_k == NULL, q (batch, seqlen_q, H, D),
+ *            k/v (batch, seqlen_k, Hkv, D); seqused_k (batch,) optionally limits each
+ *            sequence's keys (the KV-cache path, flash_attn.py:486-488).
+ *   varlen : cu_seqlens_q/k int32 (batch + 1,), packed q (total_q, H, D),
+ *            k/v (total_k, Hkv, D); max_seqlen_q/k bound the per-sequence lengths.
+ */
+typedef struct mykfa_fwd_params {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* o;
+    float* lse;
+    int64_t q_batch_stride, q_token_stride, q_head_stride;
+    int64_t k_batch_stride, k_token_stride, k_head_stride;
+    int64_t v_batch_stride, v_token_stride, v_head_stride;
+    int64_t o_batch_stride, o_token_stride, o_head_stride;
+    int64_t lse_head_stride; /* = rows */
+    const int32_t* cu_seqlens_q;
+    const int32_t* cu_seqlens_k;
+    const int32_t* seqused_k;
+    int32_t batch;
+    int32_t num_heads;
+    int32_t num_kv_heads;
+    int32_t head_dim;
+    int32_t max_seqlen_q; /* dense: seqlen_q */
+    int32_t max_seqlen_k; /* dense: seqlen_k (cache capacity on the KV-cache path) */
+    int32_t window_left;  /* >= 0; MYKFA_UNBOUNDED for none */
+    int32_t window_right; /* >= 0; 0 when causal */
+    float softmax_scale;
+    int32_t dtype; /* MYKFA_BF16 / MYKFA_FP16 */
+} mykfa_fwd_params;
+
+/*
+ * Backward parameters. Replaces the argument list of _backward / _bwd_dq_kernel /
+ * _bwd_dkdv_kernel (flash_attn.py:376-406, :181-190, :264-273). The forward fields
+ * (q, k, v, o, lse, sequence layout, window, scale) must be those of the forward call.
+ * delta is an fp32 (num_heads, rows) buffer laid out like lse.
+ */
+typedef struct mykfa_bwd_params {
+    mykfa_fwd_params fwd;
+    const void* dout;
+    void* dq;
+    void* dk;
+    void* dv;
+    float* delta;
+    int64_t do_batch_stride, do_token_stride, do_head_stride;
+    int64_t dq_batch_stride, dq_token_stride, dq_head_stride;
+    int64_t dk_batch_stride, dk_token_stride, dk_head_stride;
+    int64_t dv_batch_stride, dv_token_stride, dv_head_stride;
+} mykfa_bwd_params;
+
+/*
+ * KV-cache decode parameters (flash_attn_with_kvcache, flash_attn.py:467-490, run as a
+ * split-K forward). q (batch, seqlen_q, H, D); caches (batch, capacity, Hkv, D) with a
+ * contiguous last dimension; the keys of sequence b are cache rows [0, seqused_k[b]),
+ * clamped to [0, capacity] (all capacity rows when seqused_k is NULL).
+ * Partial results of each split go to a caller-provided workspace
+ * (mykfa_decode_workspace_size) and are combined by an LSE merge.
+ */
+typedef struct mykfa_decode_params {
+    mykfa_fwd_params fwd;   /* cu_seqlens_* must be NULL; seqused_k NULL = max_seqlen_k keys */
+    int32_t num_splits;     /* 0 = choose (mykfa_decode_num_splits) */
+} mykfa_decode_params;
+
+/* KV append: cache[b, cache_seqlens[b] + t] = new[b, t] for t < seqlen_new
+ * (flash_attn.py:480-485). */
+typedef struct mykfa_kv_append_params {
+    void* k_cache;
+    void* v_cache;
+    const void* k_new;
+    const void* v_new;
+    const int32_t* cache_seqlens;
+    int64_t kc_batch_stride, kc_token_stride, kc_head_stride;
+    int64_t vc_batch_stride, vc_token_stride, vc_head_stride;
+    int64_t kn_batch_stride, kn_token_stride, kn_head_stride;
+    int64_t vn_batch_stride, vn_token_stride, vn_head_stride;
+    int32_t batch;
+    int32_t seqlen_new;
+    int32_t capacity;
+    int32_t num_kv_heads;
+    int32_t head_dim;
+    int32_t dtype;
+} mykfa_kv_append_params;
+
+/* ---- version / errors ------------------------------------------------------------- */
+int mykfa_abi_version(void);
+const char* mykfa_version(void);
+/* Message of the last failing call on this thread ("" if none). */
+const char* mykfa_last_error(void);
+/* sizeof() of each parameter struct, so bindings can check their mirror. */
+size_t mykfa_sizeof_fwd_params(void);
+size_t mykfa_sizeof_bwd_params(void);
+size_t mykfa_sizeof_decode_params(void);
+size_t mykfa_sizeof_kv_append_params(void);
+
+/* ---- host-only validation (no GPU needed) ------------------------------------------ */
+/* Checks of _check (flash_attn.py:336-346) plus pointer/stride/window sanity. */
+int mykfa_validate_fwd(const mykfa_fwd_params* p);
+int mykfa_validate_bwd(const mykfa_bwd_params* p);
+int mykfa_validate_decode(const mykfa_decode_params* p);
+int mykfa_validate_kv_append(const mykfa_kv_append_params* p);
+
+/* ---- forward ----------------------------------------------------------------------- */
+/* O and LSE (replaces _forward + _fwd_kernel, flash_attn.py:353-373, :106-154). */
+int mykfa_fwd(const mykfa_fwd_params* p, mykfa_stream_t stream);
+
+/* ---- backward ---------------------------------------------------------------------- */
+/* delta = rowsum(dO * O) in fp32 (the preprocess fused into _bwd_dq_kernel,
+ * flash_attn.py:215-216). */
+int mykfa_bwd_preprocess(const mykfa_bwd_params* p, mykfa_stream_t stream);
+/* dK, dV summed over each GQA group (replaces _bwd_dkdv_kernel, flash_attn.py:264-314).
+ * Reads delta: run mykfa_bwd_preprocess first on the same stream. */
+int mykfa_bwd_dkdv(const mykfa_bwd_params* p, mykfa_stream_t stream);
+/* dQ (replaces the dQ part of _bwd_dq_kernel, flash_attn.py:181-230). Reads delta. */
+int mykfa_bwd_dq(const mykfa_bwd_params* p, mykfa_stream_t stream);
+/* preprocess, dK/dV and dQ in stream order (replaces _backward, flash_attn.py:376-406). */
+int mykfa_bwd(const mykfa_bwd_params* p, mykfa_stream_t stream);
+
+/* ---- KV-cache decode (split-K) ------------------------------------------------------ */
+/* Split count the library would pick for this shape (>= 1). */
+int mykfa_decode_num_splits(int32_t batch, int32_t num_kv_heads, int32_t capacity);
+/* Bytes of workspace mykfa_decode needs for this shape and split count. */
+size_t mykfa_decode_workspace_size(int32_t batch, int32_t num_heads, int32_t seqlen_q,
+                                   int32_t head_dim, int32_t num_splits);
+/* Split-K partial pass: writes per-split (O, LSE) into the workspace. */
+int mykfa_decode_splitk(const mykfa_decode_params* p, void* workspace, size_t workspace_bytes,
+                        mykfa_stream_t stream);
+/* LSE merge of the per-split partials into o and lse. */
+int mykfa_decode_merge(const mykfa_decode_params* p, const void* workspace,
+                       size_t workspace_bytes, mykfa_stream_t stream);
+/* split-K + merge (replaces _forward's decode configuration, flash_attn.py:364, :488). */
+int mykfa_decode(const mykfa_decode_params* p, void* workspace, size_t workspace_bytes,
+                 mykfa_stream_t stream);
+
+/* ---- KV append ------------------------------------------------------------------------ */
+/* Replaces the advanced-index cache writes of flash_attn_with_kvcache
+ * (flash_attn.py:480-485); graph-capturable (no host sync). */
+int mykfa_kv_append(const mykfa_kv_append_params* p, mykfa_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MYKFA_H */

@@ -1,0 +1,143 @@
+"""ctypes binding of libmykfa.so (include/mykfa.h).
+
+The structs below mirror the C parameter structs field for field; their sizes are checked
+against the library's own sizeof() at load time. Loading fails loudly when the library
+has not been built: there is no fallback implementation.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libmykfa.so"
+
+OK = 0
+ERR_INVALID = 1
+ERR_UNSUPPORTED = 2
+ERR_LAUNCH = 3
+ERR_WORKSPACE = 4
+
+DTYPE_BF16 = 0
+DTYPE_FP16 = 1
+UNBOUNDED = 1 << 30
+
+_i64, _i32, _f32, _ptr = ctypes.c_int64, ctypes.c_int32, ctypes.c_float, ctypes.c_void_p
+
+
+class FwdParams(ctypes.Structure):
+    _fields_ = [
+        ("q", _ptr), ("k", _ptr), ("v", _ptr), ("o", _ptr), ("lse", _ptr),
+        ("q_batch_stride", _i64), ("q_token_stride", _i64), ("q_head_stride", _i64),
+        ("k_batch_stride", _i64), ("k_token_stride", _i64), ("k_head_stride", _i64),
+        ("v_batch_stride", _i64), ("v_token_stride", _i64), ("v_head_stride", _i64),
+        ("o_batch_stride", _i64), ("o_token_stride", _i64), ("o_head_stride", _i64),
+        ("lse_head_stride", _i64),
+        ("cu_seqlens_q", _ptr), ("cu_seqlens_k", _ptr), ("seqused_k", _ptr),
+        ("batch", _i32), ("num_heads", _i32), ("num_kv_heads", _i32), ("head_dim", _i32),
+        ("max_seqlen_q", _i32), ("max_seqlen_k", _i32),
+        ("window_left", _i32), ("window_right", _i32),
+        ("softmax_scale", _f32), ("dtype", _i32),
+    ]
+
+
+class BwdParams(ctypes.Structure):
+    _fields_ = [
+        ("fwd", FwdParams),
+        ("dout", _ptr), ("dq", _ptr), ("dk", _ptr), ("dv", _ptr), ("delta", _ptr),
+        ("do_batch_stride", _i64), ("do_token_stride", _i64), ("do_head_stride", _i64),
+        ("dq_batch_stride", _i64), ("dq_token_stride", _i64), ("dq_head_stride", _i64),
+        ("dk_batch_stride", _i64), ("dk_token_stride", _i64), ("dk_head_stride", _i64),
+        ("dv_batch_stride", _i64), ("dv_token_stride", _i64), ("dv_head_stride", _i64),
+    ]
+
+
+class DecodeParams(ctypes.Structure):
+    _fields_ = [("fwd", FwdParams), ("num_splits", _i32)]
+
+
+class KvAppendParams(ctypes.Structure):
+    _fields_ = [
+        ("k_cache", _ptr), ("v_cache", _ptr), ("k_new", _ptr), ("v_new", _ptr), ("cache_seqlens", _ptr),
+        ("kc_batch_stride", _i64), ("kc_token_stride", _i64), ("kc_head_stride", _i64),
+        ("vc_batch_stride", _i64), ("vc_token_stride", _i64), ("vc_head_stride", _i64),
+        ("kn_batch_stride", _i64), ("kn_token_stride", _i64), ("kn_head_stride", _i64),
+        ("vn_batch_stride", _i64), ("vn_token_stride", _i64), ("vn_head_stride", _i64),
+        ("batch", _i32), ("seqlen_new", _i32), ("capacity", _i32), ("num_kv_heads", _i32),
+        ("head_dim", _i32), ("dtype", _i32),
+    ]
+
+
+# Every symbol include/mykfa.h declares, with (restype, argtypes).
+SIGNATURES = {
+    "mykfa_abi_version": (ctypes.c_int, []),
+    "mykfa_version": (ctypes.c_char_p, []),
+    "mykfa_last_error": (ctypes.c_char_p, []),
+    "mykfa_sizeof_fwd_params": (ctypes.c_size_t, []),
+    "mykfa_sizeof_bwd_params": (ctypes.c_size_t, []),
+    "mykfa_sizeof_decode_params": (ctypes.c_size_t, []),
+    "mykfa_sizeof_kv_append_params": (ctypes.c_size_t, []),
+    "mykfa_validate_fwd": (ctypes.c_int, [ctypes.POINTER(FwdParams)]),
+    "mykfa_validate_bwd": (ctypes.c_int, [ctypes.POINTER(BwdParams)]),
+    "mykfa_validate_decode": (ctypes.c_int, [ctypes.POINTER(DecodeParams)]),
+    "mykfa_validate_kv_append": (ctypes.c_int, [ctypes.POINTER(KvAppendParams)]),
+    "mykfa_fwd": (ctypes.c_int, [ctypes.POINTER(FwdParams), _ptr]),
+    "mykfa_bwd_preprocess": (ctypes.c_int, [ctypes.POINTER(BwdParams), _ptr]),
+    "mykfa_bwd_dkdv": (ctypes.c_int, [ctypes.POINTER(BwdParams), _ptr]),
+    "mykfa_bwd_dq": (ctypes.c_int, [ctypes.POINTER(BwdParams), _ptr]),
+    "mykfa_bwd": (ctypes.c_int, [ctypes.POINTER(BwdParams), _ptr]),
+    "mykfa_decode_num_splits": (ctypes.c_int, [_i32, _i32, _i32]),
+    "mykfa_decode_workspace_size": (ctypes.c_size_t, [_i32, _i32, _i32, _i32, _i32]),
+    "mykfa_decode_splitk": (ctypes.c_int, [ctypes.POINTER(DecodeParams), _ptr, ctypes.c_size_t, _ptr]),
+    "mykfa_decode_merge": (ctypes.c_int, [ctypes.POINTER(DecodeParams), _ptr, ctypes.c_size_t, _ptr]),
+    "mykfa_decode": (ctypes.c_int, [ctypes.POINTER(DecodeParams), _ptr, ctypes.c_size_t, _ptr]),
+    "mykfa_kv_append": (ctypes.c_int, [ctypes.POINTER(KvAppendParams), _ptr]),
+}
+
+_STRUCT_SIZES = {
+    "mykfa_sizeof_fwd_params": FwdParams,
+    "mykfa_sizeof_bwd_params": BwdParams,
+    "mykfa_sizeof_decode_params": DecodeParams,
+    "mykfa_sizeof_kv_append_params": KvAppendParams,
+}
+
+_lib: ctypes.CDLL | None = None
+
+
+class MykfaError(RuntimeError):
+    """A libmykfa call returned a non-zero status."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"mykfa error {code}: {message}")
+        self.code = code
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library; raises if libmykfa.so was not built (no fallback path exists)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = os.environ.get("MYKFA_LIB", str(LIB_PATH))
+    if not os.path.exists(path):
+        raise RuntimeError(
+            f"{path} is missing: the gfx950 FlashAttention library must be built first "
+            "(python -m myk_llm_amd.build); there is no fallback implementation")
+    handle = ctypes.CDLL(path)
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    if handle.mykfa_abi_version() != 1:
+        raise RuntimeError(f"{path}: ABI version {handle.mykfa_abi_version()} != 1")
+    for name, struct in _STRUCT_SIZES.items():
+        size = getattr(handle, name)()
+        if size != ctypes.sizeof(struct):
+            raise RuntimeError(f"{path}: {struct.__name__} is {size} bytes in C, {ctypes.sizeof(struct)} here")
+    _lib = handle
+    return handle
+
+
+def check(code: int) -> None:
+    if code != OK:
+        raise MykfaError(code, lib().mykfa_last_error().decode())

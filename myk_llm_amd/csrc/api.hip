@@ -1,0 +1,254 @@
+// C ABI of libmykfa: argument validation (host only, usable without a GPU), error
+// reporting, and dispatch to the kernel launchers. Nothing here allocates device memory or
+// synchronizes; launches go to the caller's stream.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <string>
+
+#include "kernels.h"
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_error = buf;
+    return code;
+}
+
+int ok() {
+    g_error.clear();
+    return MYKFA_OK;
+}
+
+int launched(hipError_t e, const char* what) {
+    if (e != hipSuccess) return fail(MYKFA_ERR_LAUNCH, "%s: HIP launch failed: %s", what, hipGetErrorString(e));
+    return ok();
+}
+
+bool head_dim_supported(int d) { return d == 16 || d == 32 || d == 64 || d == 128 || d == 256; }
+
+// Kernels use 16-byte vector accesses along head_dim: base pointers must be 16-byte aligned
+// and every stride a multiple of 8 elements.
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+bool stride_ok(int64_t s) { return s >= 0 && (s & 7) == 0; }
+
+int check_tensor(const void* ptr, int64_t bs, int64_t ts, int64_t hs, const char* name, bool needed) {
+    if (!needed) return MYKFA_OK;
+    if (ptr == nullptr) return fail(MYKFA_ERR_INVALID, "%s is NULL", name);
+    if (!aligned16(ptr)) return fail(MYKFA_ERR_INVALID, "%s must be 16-byte aligned", name);
+    if (!stride_ok(bs) || !stride_ok(ts) || !stride_ok(hs))
+        return fail(MYKFA_ERR_INVALID,
+                    "%s strides (%lld, %lld, %lld) must be non-negative multiples of 8 elements", name,
+                    (long long)bs, (long long)ts, (long long)hs);
+    return MYKFA_OK;
+}
+
+// flash_attn.py:336-346 (_check) and the layout rules of _forward (:358-363).
+int check_fwd(const mykfa_fwd_params* p) {
+    if (p == nullptr) return fail(MYKFA_ERR_INVALID, "params is NULL");
+    if (p->dtype != MYKFA_BF16 && p->dtype != MYKFA_FP16)
+        return fail(MYKFA_ERR_UNSUPPORTED, "flash attention needs bf16/fp16 q, k, v; got dtype code %d", p->dtype);
+    if (!head_dim_supported(p->head_dim))
+        return fail(MYKFA_ERR_UNSUPPORTED, "head_dim must be one of [16, 32, 64, 128, 256]; got %d", p->head_dim);
+    if (p->num_heads <= 0 || p->num_kv_heads <= 0 || p->num_heads % p->num_kv_heads != 0)
+        return fail(MYKFA_ERR_INVALID, "query heads (%d) must be a multiple of key/value heads (%d)", p->num_heads,
+                    p->num_kv_heads);
+    if (p->num_heads > 65535 * 4)
+        return fail(MYKFA_ERR_UNSUPPORTED, "num_heads %d exceeds the grid limit", p->num_heads);
+    if (p->batch < 0 || p->max_seqlen_q < 0 || p->max_seqlen_k < 0)
+        return fail(MYKFA_ERR_INVALID, "negative batch (%d) or sequence length (%d, %d)", p->batch, p->max_seqlen_q,
+                    p->max_seqlen_k);
+    if (p->batch > 65535) return fail(MYKFA_ERR_UNSUPPORTED, "batch %d exceeds the grid limit 65535", p->batch);
+    if (p->window_left < 0 || p->window_right < 0 || p->window_left > MYKFA_UNBOUNDED ||
+        p->window_right > MYKFA_UNBOUNDED)
+        return fail(MYKFA_ERR_INVALID, "window sides must lie in [0, 2^30]; got (%d, %d)", p->window_left,
+                    p->window_right);
+    if (!(p->softmax_scale == p->softmax_scale)) return fail(MYKFA_ERR_INVALID, "softmax_scale is NaN");
+    const bool varlen_q = p->cu_seqlens_q != nullptr, varlen_k = p->cu_seqlens_k != nullptr;
+    if (varlen_q != varlen_k)
+        return fail(MYKFA_ERR_INVALID, "cu_seqlens_q and cu_seqlens_k must both be given or both be NULL");
+    if (varlen_q && p->seqused_k != nullptr)
+        return fail(MYKFA_ERR_INVALID, "seqused_k applies to the dense layout only");
+    if (varlen_q && (p->q_batch_stride != 0 || p->k_batch_stride != 0 || p->v_batch_stride != 0 ||
+                     p->o_batch_stride != 0))
+        return fail(MYKFA_ERR_INVALID, "packed (varlen) tensors must have batch stride 0");
+    const bool work = p->batch > 0 && p->max_seqlen_q > 0;
+    int rc;
+    if ((rc = check_tensor(p->q, p->q_batch_stride, p->q_token_stride, p->q_head_stride, "q", work))) return rc;
+    if ((rc = check_tensor(p->o, p->o_batch_stride, p->o_token_stride, p->o_head_stride, "o", work))) return rc;
+    const bool keys = work && p->max_seqlen_k > 0;
+    if ((rc = check_tensor(p->k, p->k_batch_stride, p->k_token_stride, p->k_head_stride, "k", keys))) return rc;
+    if ((rc = check_tensor(p->v, p->v_batch_stride, p->v_token_stride, p->v_head_stride, "v", keys))) return rc;
+    if (work && p->lse == nullptr) return fail(MYKFA_ERR_INVALID, "lse is NULL");
+    if (work && p->lse_head_stride < (varlen_q ? 0 : (int64_t)p->batch * p->max_seqlen_q))
+        return fail(MYKFA_ERR_INVALID, "lse_head_stride %lld is smaller than the number of rows",
+                    (long long)p->lse_head_stride);
+    return ok();
+}
+
+int check_bwd(const mykfa_bwd_params* p) {
+    if (p == nullptr) return fail(MYKFA_ERR_INVALID, "params is NULL");
+    int rc = check_fwd(&p->fwd);
+    if (rc) return rc;
+    if (p->fwd.seqused_k != nullptr) return fail(MYKFA_ERR_INVALID, "the backward pass takes no seqused_k");
+    const bool work = p->fwd.batch > 0 && p->fwd.max_seqlen_q > 0;
+    const bool keys = p->fwd.batch > 0 && p->fwd.max_seqlen_k > 0;
+    if ((rc = check_tensor(p->dout, p->do_batch_stride, p->do_token_stride, p->do_head_stride, "dout", work))) return rc;
+    if ((rc = check_tensor(p->dq, p->dq_batch_stride, p->dq_token_stride, p->dq_head_stride, "dq", work))) return rc;
+    if ((rc = check_tensor(p->dk, p->dk_batch_stride, p->dk_token_stride, p->dk_head_stride, "dk", keys))) return rc;
+    if ((rc = check_tensor(p->dv, p->dv_batch_stride, p->dv_token_stride, p->dv_head_stride, "dv", keys))) return rc;
+    if (work && p->delta == nullptr) return fail(MYKFA_ERR_INVALID, "delta is NULL");
+    if (p->fwd.cu_seqlens_q != nullptr &&
+        (p->do_batch_stride != 0 || p->dq_batch_stride != 0 || p->dk_batch_stride != 0 || p->dv_batch_stride != 0))
+        return fail(MYKFA_ERR_INVALID, "packed (varlen) gradients must have batch stride 0");
+    return ok();
+}
+
+int check_decode(const mykfa_decode_params* p) {
+    if (p == nullptr) return fail(MYKFA_ERR_INVALID, "params is NULL");
+    int rc = check_fwd(&p->fwd);
+    if (rc) return rc;
+    if (p->fwd.cu_seqlens_q != nullptr) return fail(MYKFA_ERR_INVALID, "decode takes the dense layout only");
+    if (p->num_splits < 0 || p->num_splits > 1024)
+        return fail(MYKFA_ERR_INVALID, "num_splits must lie in [0, 1024]; got %d", p->num_splits);
+    return ok();
+}
+
+int check_append(const mykfa_kv_append_params* p) {
+    if (p == nullptr) return fail(MYKFA_ERR_INVALID, "params is NULL");
+    if (p->dtype != MYKFA_BF16 && p->dtype != MYKFA_FP16)
+        return fail(MYKFA_ERR_UNSUPPORTED, "kv append needs bf16/fp16 caches; got dtype code %d", p->dtype);
+    if (!head_dim_supported(p->head_dim))
+        return fail(MYKFA_ERR_UNSUPPORTED, "head_dim must be one of [16, 32, 64, 128, 256]; got %d", p->head_dim);
+    if (p->batch < 0 || p->seqlen_new < 0 || p->capacity < 0 || p->num_kv_heads <= 0)
+        return fail(MYKFA_ERR_INVALID, "invalid kv append shape");
+    if (p->batch > 65535) return fail(MYKFA_ERR_UNSUPPORTED, "batch %d exceeds the grid limit 65535", p->batch);
+    const bool work = p->batch > 0 && p->seqlen_new > 0;
+    if (work && p->cache_seqlens == nullptr) return fail(MYKFA_ERR_INVALID, "cache_seqlens is NULL");
+    int rc;
+    if ((rc = check_tensor(p->k_cache, p->kc_batch_stride, p->kc_token_stride, p->kc_head_stride, "k_cache", work))) return rc;
+    if ((rc = check_tensor(p->v_cache, p->vc_batch_stride, p->vc_token_stride, p->vc_head_stride, "v_cache", work))) return rc;
+    if ((rc = check_tensor(p->k_new, p->kn_batch_stride, p->kn_token_stride, p->kn_head_stride, "k", work))) return rc;
+    if ((rc = check_tensor(p->v_new, p->vn_batch_stride, p->vn_token_stride, p->vn_head_stride, "v", work))) return rc;
+    return ok();
+}
+
+hipStream_t as_stream(mykfa_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+int choose_splits(const mykfa_decode_params* p) {
+    return p->num_splits > 0 ? p->num_splits
+                             : mykfa::decode_default_splits(p->fwd.batch, p->fwd.num_kv_heads, p->fwd.max_seqlen_k);
+}
+
+}  // namespace
+
+extern "C" {
+
+int mykfa_abi_version(void) { return MYKFA_ABI_VERSION; }
+const char* mykfa_version(void) { return "mykfa 0.1.0 (gfx950)"; }
+const char* mykfa_last_error(void) { return g_error.c_str(); }
+size_t mykfa_sizeof_fwd_params(void) { return sizeof(mykfa_fwd_params); }
+size_t mykfa_sizeof_bwd_params(void) { return sizeof(mykfa_bwd_params); }
+size_t mykfa_sizeof_decode_params(void) { return sizeof(mykfa_decode_params); }
+size_t mykfa_sizeof_kv_append_params(void) { return sizeof(mykfa_kv_append_params); }
+
+int mykfa_validate_fwd(const mykfa_fwd_params* p) { return check_fwd(p); }
+int mykfa_validate_bwd(const mykfa_bwd_params* p) { return check_bwd(p); }
+int mykfa_validate_decode(const mykfa_decode_params* p) { return check_decode(p); }
+int mykfa_validate_kv_append(const mykfa_kv_append_params* p) { return check_append(p); }
+
+int mykfa_fwd(const mykfa_fwd_params* p, mykfa_stream_t stream) {
+    int rc = check_fwd(p);
+    if (rc) return rc;
+    if (p->batch == 0 || p->max_seqlen_q == 0) return ok();
+    return launched(mykfa::launch_fwd(*p, as_stream(stream)), "mykfa_fwd");
+}
+
+int mykfa_bwd_preprocess(const mykfa_bwd_params* p, mykfa_stream_t stream) {
+    int rc = check_bwd(p);
+    if (rc) return rc;
+    if (p->fwd.batch == 0 || p->fwd.max_seqlen_q == 0) return ok();
+    return launched(mykfa::launch_bwd_preprocess(*p, as_stream(stream)), "mykfa_bwd_preprocess");
+}
+
+int mykfa_bwd_dkdv(const mykfa_bwd_params* p, mykfa_stream_t stream) {
+    int rc = check_bwd(p);
+    if (rc) return rc;
+    if (p->fwd.batch == 0 || p->fwd.max_seqlen_k == 0) return ok();
+    return launched(mykfa::launch_bwd_dkdv(*p, as_stream(stream)), "mykfa_bwd_dkdv");
+}
+
+int mykfa_bwd_dq(const mykfa_bwd_params* p, mykfa_stream_t stream) {
+    int rc = check_bwd(p);
+    if (rc) return rc;
+    if (p->fwd.batch == 0 || p->fwd.max_seqlen_q == 0) return ok();
+    return launched(mykfa::launch_bwd_dq(*p, as_stream(stream)), "mykfa_bwd_dq");
+}
+
+int mykfa_bwd(const mykfa_bwd_params* p, mykfa_stream_t stream) {
+    int rc = mykfa_bwd_preprocess(p, stream);
+    if (rc) return rc;
+    rc = mykfa_bwd_dkdv(p, stream);
+    if (rc) return rc;
+    return mykfa_bwd_dq(p, stream);
+}
+
+int mykfa_decode_num_splits(int32_t batch, int32_t num_kv_heads, int32_t capacity) {
+    return mykfa::decode_default_splits(batch, num_kv_heads, capacity);
+}
+
+size_t mykfa_decode_workspace_size(int32_t batch, int32_t num_heads, int32_t seqlen_q, int32_t head_dim,
+                                   int32_t num_splits) {
+    if (batch < 0 || num_heads < 0 || seqlen_q < 0 || head_dim < 0 || num_splits < 0) return 0;
+    return mykfa::decode_workspace_bytes(batch, num_heads, seqlen_q, head_dim, num_splits);
+}
+
+int mykfa_decode_splitk(const mykfa_decode_params* p, void* workspace, size_t workspace_bytes,
+                        mykfa_stream_t stream) {
+    int rc = check_decode(p);
+    if (rc) return rc;
+    if (p->fwd.batch == 0 || p->fwd.max_seqlen_q == 0) return ok();
+    const int splits = choose_splits(p);
+    const size_t need = mykfa::decode_workspace_bytes(p->fwd.batch, p->fwd.num_heads, p->fwd.max_seqlen_q,
+                                                      p->fwd.head_dim, splits);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+        return fail(MYKFA_ERR_WORKSPACE, "decode workspace needs %zu bytes; got %zu", need, workspace_bytes);
+    if (!aligned16(workspace)) return fail(MYKFA_ERR_INVALID, "workspace must be 16-byte aligned");
+    return launched(mykfa::launch_decode_splitk(*p, splits, workspace, as_stream(stream)), "mykfa_decode_splitk");
+}
+
+int mykfa_decode_merge(const mykfa_decode_params* p, const void* workspace, size_t workspace_bytes,
+                       mykfa_stream_t stream) {
+    int rc = check_decode(p);
+    if (rc) return rc;
+    if (p->fwd.batch == 0 || p->fwd.max_seqlen_q == 0) return ok();
+    const int splits = choose_splits(p);
+    const size_t need = mykfa::decode_workspace_bytes(p->fwd.batch, p->fwd.num_heads, p->fwd.max_seqlen_q,
+                                                      p->fwd.head_dim, splits);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+        return fail(MYKFA_ERR_WORKSPACE, "decode workspace needs %zu bytes; got %zu", need, workspace_bytes);
+    return launched(mykfa::launch_decode_merge(*p, splits, workspace, as_stream(stream)), "mykfa_decode_merge");
+}
+
+int mykfa_decode(const mykfa_decode_params* p, void* workspace, size_t workspace_bytes, mykfa_stream_t stream) {
+    int rc = mykfa_decode_splitk(p, workspace, workspace_bytes, stream);
+    if (rc) return rc;
+    if (choose_splits(p) == 1) return ok();  // a single split writes o and lse directly
+    return mykfa_decode_merge(p, workspace, workspace_bytes, stream);
+}
+
+int mykfa_kv_append(const mykfa_kv_append_params* p, mykfa_stream_t stream) {
+    int rc = check_append(p);
+    if (rc) return rc;
+    if (p->batch == 0 || p->seqlen_new == 0) return ok();
+    return launched(mykfa::launch_kv_append(*p, as_stream(stream)), "mykfa_kv_append");
+}
+
+}  // extern "C"

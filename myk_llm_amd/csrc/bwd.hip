@@ -1,0 +1,581 @@
+// Backward pass (replaces _bwd_dq_kernel and _bwd_dkdv_kernel, flash_attn.py:157-314).
+// Three launches in stream order, no atomics (results are bitwise deterministic):
+//   1. preprocess: delta = rowsum(dO * O) in fp32                 (flash_attn.py:215-216)
+//   2. dK/dV: one workgroup per 128-key block of one KV head; K and V stay in registers as
+//      MFMA B operands while the workgroup streams the query tiles of EVERY query head of
+//      the GQA group through LDS, so K/V are read once per group (flash_attn.py:300-311).
+//      Per 32-query step a wave computes S = Q K^T and dP = dO V^T (A operands: row reads
+//      of the LDS Q/dO tiles), P = exp2(S * c - lse), dS = P (dP - delta), then
+//      dV^T += dO^T P and dK^T += Q^T dS with dO^T / Q^T taken by the LDS transpose read.
+//   3. dQ: forward-shaped: S^T = K Q^T, dP^T = V dO^T, dS^T = P^T (dP^T - delta), then
+//      dQ^T += K^T dS^T with K^T read transposed from the LDS K tile.
+// All products are 32x32x16 bf16 (or fp16) MFMA with fp32 accumulation; P and dS are
+// rounded to the input type before their products, as in flash_attn.py:177, :257, :260.
+#include "common.h"
+#include "kernels.h"
+
+namespace mykfa {
+
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+
+struct BwdArgs {
+    const uint16_t* q;
+    const uint16_t* k;
+    const uint16_t* v;
+    const uint16_t* o;
+    const uint16_t* dout;
+    uint16_t* dq;
+    uint16_t* dk;
+    uint16_t* dv;
+    const float* lse;
+    float* delta;
+    int64_t qbs, qts, qhs, kbs, kts, khs, vbs, vts, vhs, obs, ots, ohs;
+    int64_t dobs, dots, dohs, dqbs, dqts, dqhs, dkbs, dkts, dkhs, dvbs, dvts, dvhs;
+    int64_t lse_hs;
+    const int32_t* cu_q;
+    const int32_t* cu_k;
+    int seqlen_q, seqlen_k;
+    int wl, wr;
+    float qk_scale;
+    float sm_scale;
+    int group;
+    int hpw;
+    int num_heads;
+    int batch;
+};
+
+// ---- 1. delta = rowsum(dO * O) ---------------------------------------------------------
+
+template <int D, typename T>
+__global__ __launch_bounds__(256) void bwd_preprocess_kernel(BwdArgs a) {
+    constexpr int CPR = D / 8;         // lanes per (token, head) row
+    constexpr int RPB = 256 / CPR;     // rows per block
+    const int b = blockIdx.y;
+    SeqInfo qs = seq_info(b, a.cu_q, nullptr, a.seqlen_q, false);
+    const int64_t item = (int64_t)blockIdx.x * RPB + threadIdx.x / CPR;  // over (token, head)
+    const int ch = threadIdx.x % CPR;
+    const int tok = item / a.num_heads, h = item % a.num_heads;
+    float s = 0.f;
+    const bool ok_row = tok < qs.len;
+    if (ok_row) {
+        const uint16_t* op = a.o + (int64_t)b * a.obs + (qs.tok0 + tok) * a.ots + (int64_t)h * a.ohs + ch * 8;
+        const uint16_t* dp = a.dout + (int64_t)b * a.dobs + (qs.tok0 + tok) * a.dots + (int64_t)h * a.dohs + ch * 8;
+        s16x8 ov = ld16(op), dv = ld16(dp);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s += T::to_float((uint16_t)ov[i]) * T::to_float((uint16_t)dv[i]);
+    }
+#pragma unroll
+    for (int off = 1; off < CPR; off <<= 1) s += __shfl_xor(s, off);
+    if (ok_row && ch == 0) a.delta[(int64_t)h * a.lse_hs + qs.row0 + tok] = s;
+}
+
+// ---- 2. dK / dV -------------------------------------------------------------------------
+
+template <int D>
+struct RowTileLoader {  // BM x D tile of a (token, head) tensor, rows beyond len are zero
+    static constexpr int CPR = D / 8;
+    static constexpr int BM = 32;
+    static constexpr int CHUNKS = BM * CPR;
+    static constexpr int PER = (CHUNKS + kThreads - 1) / kThreads;
+    s16x8 r[PER];
+    __device__ inline void load(const uint16_t* base, int64_t tstride, int m0, int len, int tid) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int idx = tid + i * kThreads;
+            const int row = idx / CPR, ch = idx % CPR;
+            s16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
+            if ((CHUNKS % kThreads == 0 || idx < CHUNKS) && m0 + row < len)
+                v = ld16(base + (int64_t)(m0 + row) * tstride + ch * 8);
+            r[i] = v;
+        }
+    }
+    __device__ inline void store(uint16_t* lds, int tid) const {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int idx = tid + i * kThreads;
+            if (CHUNKS % kThreads == 0 || idx < CHUNKS) {
+                const int row = idx / CPR, ch = idx % CPR;
+                *reinterpret_cast<s16x8*>(lds + row * D + ((ch ^ lds_swz<D>(row)) << 3)) = r[i];
+            }
+        }
+    }
+};
+
+// A operand (32 rows x 16 k) of a row-major LDS tile at rows perm32(l32), k-step kk.
+template <int D>
+__device__ inline s16x8 lds_row_op(const uint16_t* tile, int rbase, int l32, int g, int kk) {
+    const int row = rbase + perm32(l32);
+    return *reinterpret_cast<const s16x8*>(tile + row * D + (((2 * kk + g) ^ lds_swz<D>(row)) << 3));
+}
+
+// A operand (32 columns d x 16 rows) of the transposed LDS tile: lane holds
+// tile[16 kb + 8 g + i][32 db + l32], through two transpose reads. Columns beyond D read 0.
+template <int D>
+__device__ inline s16x8 lds_tr_op(const uint16_t* tile, int db, int kb, int lane) {
+    const int G = lane >> 4, jj = lane & 15;
+    int col = 32 * db + 16 * (G & 1) + 4 * (jj & 3);
+    const bool valid = col < D;
+    if (!valid) col = col % D;
+    const int row = 16 * kb + 8 * (G >> 1) + (jj >> 2);
+    s16x8 v = cat4(ds_read_tr(tile + lds_off<D>(row, col)), ds_read_tr(tile + lds_off<D>(row + 4, col)));
+    if (!valid) v = s16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    return v;
+}
+
+template <int D, typename T>
+__global__ __launch_bounds__(kThreads) void bwd_dkdv_kernel(BwdArgs a) {
+    constexpr int KD = D / 16;
+    constexpr int DB = (D + 31) / 32;
+    constexpr int BMQ = 32;           // queries per step
+    constexpr int BNK = 32 * kWaves;  // keys per workgroup
+    __shared__ __attribute__((aligned(16))) uint16_t sq[2][BMQ * D];
+    __shared__ __attribute__((aligned(16))) uint16_t sdo[2][BMQ * D];
+    __shared__ __attribute__((aligned(16))) float slse[2][BMQ];
+    __shared__ __attribute__((aligned(16))) float sdel[2][BMQ];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int l32 = lane & 31, g = lane >> 5;
+    const int n0 = blockIdx.x * BNK;  // causal: the first key blocks see the most queries
+    const int b = blockIdx.y, kvh = blockIdx.z;
+    SeqInfo ks = seq_info(b, a.cu_k, nullptr, a.seqlen_k, false);
+    const int k_len = ks.len;
+    if (n0 >= k_len) return;
+    SeqInfo qs = seq_info(b, a.cu_q, nullptr, a.seqlen_q, false);
+    const int q_len = qs.len;
+    // Query i sees key j iff (i - j) in [q_len - k_len - wr, q_len - k_len + wl]
+    // (flash_attn.py:294-296); forward-oriented offsets for the element mask.
+    const int lo_t = band_lo(q_len, k_len, a.wr), hi_t = band_hi(q_len, k_len, a.wl);
+    const int lo_f = band_lo(k_len, q_len, a.wl), hi_f = band_hi(k_len, q_len, a.wr);
+
+    const int wg_bs = k_len - n0 < BNK ? k_len - n0 : BNK;
+    const Ranges wgr = block_ranges(n0, wg_bs, lo_t, hi_t, q_len, BMQ);
+    const int nw0 = n0 + 32 * wave;
+    const int bs = k_len - nw0 < 32 ? k_len - nw0 : 32;
+    Ranges wr = {0, 0, 0, 0};
+    if (bs > 0) wr = block_ranges(nw0, bs, lo_t, hi_t, q_len, BMQ);
+
+    // K, V rows of this wave as B operands: lane holds K[nw0 + l32][16 kk + 8 g + i].
+    s16x8 kop[KD], vop[KD];
+    {
+        const int key = nw0 + l32;
+        const uint16_t* kp = a.k + (int64_t)b * a.kbs + (ks.tok0 + key) * a.kts + (int64_t)kvh * a.khs;
+        const uint16_t* vp = a.v + (int64_t)b * a.vbs + (ks.tok0 + key) * a.vts + (int64_t)kvh * a.vhs;
+#pragma unroll
+        for (int kk = 0; kk < KD; ++kk) {
+            s16x8 z = {0, 0, 0, 0, 0, 0, 0, 0};
+            kop[kk] = key < k_len ? ld16(kp + 16 * kk + 8 * g) : z;
+            vop[kk] = key < k_len ? ld16(vp + 16 * kk + 8 * g) : z;
+        }
+    }
+    f32x16 dk[DB], dv[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dk[db][r] = dv[db][r] = 0.f;
+
+    const int ntiles = wgr.hi > wgr.lo ? (wgr.hi - wgr.lo + BMQ - 1) / BMQ : 0;
+    const int iters = ntiles * a.group;
+    RowTileLoader<D> ql, dol;
+    float lse_r = 0.f, del_r = 0.f;
+    auto issue = [&](int it) {
+        const int hg = it / ntiles, m0 = wgr.lo + (it % ntiles) * BMQ;
+        const int h = kvh * a.group + hg;
+        ql.load(a.q + (int64_t)b * a.qbs + qs.tok0 * a.qts + (int64_t)h * a.qhs, a.qts, m0, q_len, tid);
+        dol.load(a.dout + (int64_t)b * a.dobs + qs.tok0 * a.dots + (int64_t)h * a.dohs, a.dots, m0, q_len, tid);
+        if (tid < 2 * BMQ) {
+            const int r = tid & (BMQ - 1);
+            const bool ok = m0 + r < q_len;
+            const int64_t off = (int64_t)h * a.lse_hs + qs.row0 + m0 + r;
+            if (tid < BMQ) lse_r = ok ? a.lse[off] : INFINITY;
+            else del_r = ok ? a.delta[off] : 0.f;
+        }
+    };
+    auto commit = [&](int buf) {
+        ql.store(sq[buf], tid);
+        dol.store(sdo[buf], tid);
+        if (tid < BMQ) slse[buf][tid] = lse_r;
+        else if (tid < 2 * BMQ) sdel[buf][tid - BMQ] = del_r;
+    };
+    if (iters > 0) {
+        issue(0);
+        commit(0);
+    }
+    int buf = 0;
+    for (int it = 0; it < iters; ++it) {
+        __syncthreads();
+        const bool more = it + 1 < iters;
+        if (more) issue(it + 1);
+        const int m0 = wgr.lo + (it % ntiles) * BMQ;
+        const bool active = bs > 0 && m0 < wr.hi && m0 + BMQ > wr.lo;
+        if (active) {
+            const bool masked = !(m0 >= wr.mid_lo && m0 + BMQ <= wr.mid_hi);
+            const uint16_t* Qs = sq[buf];
+            const uint16_t* DOs = sdo[buf];
+            // S = Q K^T and dP = dO V^T: lane column = key nw0 + l32, registers = queries.
+            f32x16 s, dp;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
+#pragma unroll
+            for (int kk = 0; kk < KD; ++kk) {
+                s = T::mfma32(lds_row_op<D>(Qs, 0, l32, g, kk), kop[kk], s);
+                dp = T::mfma32(lds_row_op<D>(DOs, 0, l32, g, kk), vop[kk], dp);
+            }
+            const int key = nw0 + l32;
+            s16x8 pb[2], dsb[2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                // Rows 16 kb + 8 g + i, i = 0..7 (registers 8 kb + i).
+                const f32x4 l0 = *reinterpret_cast<const f32x4*>(&slse[buf][16 * kb + 8 * g]);
+                const f32x4 l1 = *reinterpret_cast<const f32x4*>(&slse[buf][16 * kb + 8 * g + 4]);
+                const f32x4 d0 = *reinterpret_cast<const f32x4*>(&sdel[buf][16 * kb + 8 * g]);
+                const f32x4 d1 = *reinterpret_cast<const f32x4*>(&sdel[buf][16 * kb + 8 * g + 4]);
+                float pv[8], dsv[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float lse_i = i < 4 ? l0[i] : l1[i - 4];
+                    const float del_i = i < 4 ? d0[i] : d1[i - 4];
+                    float p = fast_exp2(s[8 * kb + i] * a.qk_scale - lse_i);
+                    if (masked) {
+                        const int qi = m0 + 16 * kb + 8 * g + i;
+                        const int rel = key - qi;
+                        p = (rel >= lo_f && rel <= hi_f && qi < q_len && key < k_len) ? p : 0.f;
+                    }
+                    pv[i] = p;
+                    dsv[i] = p * (dp[8 * kb + i] - del_i);
+                }
+                u32x4 pw = {T::pack2(pv[0], pv[1]), T::pack2(pv[2], pv[3]), T::pack2(pv[4], pv[5]),
+                            T::pack2(pv[6], pv[7])};
+                u32x4 dw = {T::pack2(dsv[0], dsv[1]), T::pack2(dsv[2], dsv[3]), T::pack2(dsv[4], dsv[5]),
+                            T::pack2(dsv[6], dsv[7])};
+                pb[kb] = __builtin_bit_cast(s16x8, pw);
+                dsb[kb] = __builtin_bit_cast(s16x8, dw);
+            }
+            // dV^T += dO^T P, dK^T += Q^T dS.
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+                    dv[db] = T::mfma32(lds_tr_op<D>(DOs, db, kb, lane), pb[kb], dv[db]);
+                    dk[db] = T::mfma32(lds_tr_op<D>(Qs, db, kb, lane), dsb[kb], dk[db]);
+                }
+        }
+        if (more) commit(buf ^ 1);
+        buf ^= 1;
+    }
+
+    // Store dK * sm_scale and dV (flash_attn.py:312-314); lane column = key, rows = d.
+    const int key = nw0 + l32;
+    if (bs > 0 && key < k_len) {
+        uint16_t* dkp = a.dk + (int64_t)b * a.dkbs + (ks.tok0 + key) * a.dkts + (int64_t)kvh * a.dkhs;
+        uint16_t* dvp = a.dv + (int64_t)b * a.dvbs + (ks.tok0 + key) * a.dvts + (int64_t)kvh * a.dvhs;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int rq = 0; rq < 4; ++rq) {
+                const int d0 = 32 * db + 8 * rq + 4 * g;
+                if (d0 < D) {
+                    u32x2 wk = {T::pack2(dk[db][4 * rq] * a.sm_scale, dk[db][4 * rq + 1] * a.sm_scale),
+                                T::pack2(dk[db][4 * rq + 2] * a.sm_scale, dk[db][4 * rq + 3] * a.sm_scale)};
+                    u32x2 wv = {T::pack2(dv[db][4 * rq], dv[db][4 * rq + 1]),
+                                T::pack2(dv[db][4 * rq + 2], dv[db][4 * rq + 3])};
+                    *reinterpret_cast<u32x2*>(dkp + d0) = wk;
+                    *reinterpret_cast<u32x2*>(dvp + d0) = wv;
+                }
+            }
+    }
+}
+
+// ---- 3. dQ ------------------------------------------------------------------------------
+
+template <int D, int BN>
+struct KeyTileLoader {
+    static constexpr int CPR = D / 8;
+    static constexpr int CHUNKS = BN * CPR;
+    static constexpr int PER = (CHUNKS + kThreads - 1) / kThreads;
+    s16x8 r[PER];
+    __device__ inline void load(const uint16_t* base, int64_t tstride, int n0, int len, int tid) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int idx = tid + i * kThreads;
+            const int row = idx / CPR, ch = idx % CPR;
+            s16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
+            if ((CHUNKS % kThreads == 0 || idx < CHUNKS) && n0 + row < len)
+                v = ld16(base + (int64_t)(n0 + row) * tstride + ch * 8);
+            r[i] = v;
+        }
+    }
+    __device__ inline void store(uint16_t* lds, int tid) const {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int idx = tid + i * kThreads;
+            if (CHUNKS % kThreads == 0 || idx < CHUNKS) {
+                const int row = idx / CPR, ch = idx % CPR;
+                *reinterpret_cast<s16x8*>(lds + row * D + ((ch ^ lds_swz<D>(row)) << 3)) = r[i];
+            }
+        }
+    }
+};
+
+template <int D, int BN, typename T>
+__global__ __launch_bounds__(kThreads) void bwd_dq_kernel(BwdArgs a) {
+    constexpr int KD = D / 16;
+    constexpr int DB = (D + 31) / 32;
+    constexpr int NB = BN / 32;
+    constexpr int KB = BN / 16;
+    __shared__ __attribute__((aligned(16))) uint16_t smem[2][2][BN * D];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int l32 = lane & 31, g = lane >> 5;
+    const int tpw = kWaves / a.hpw;
+    const int mblk = gridDim.x - 1 - blockIdx.x;
+    const int b = blockIdx.y;
+    const int h_first = blockIdx.z * a.hpw;
+    SeqInfo qs = seq_info(b, a.cu_q, nullptr, a.seqlen_q, false);
+    const int tok_base = mblk * tpw * 32;
+    if (tok_base >= qs.len) return;
+    SeqInfo ks = seq_info(b, a.cu_k, nullptr, a.seqlen_k, false);
+    const int q_len = qs.len, k_len = ks.len;
+    const int kvh = h_first / a.group;
+    const int lo_off = band_lo(k_len, q_len, a.wl), hi_off = band_hi(k_len, q_len, a.wr);
+
+    int wg_lo = 1 << 30, wg_hi = 0;
+    for (int tb = 0; tb < tpw; ++tb) {
+        const int s0 = tok_base + tb * 32;
+        const int bs = q_len - s0 < 32 ? q_len - s0 : 32;
+        if (bs <= 0) continue;
+        Ranges r = block_ranges(s0, bs, lo_off, hi_off, k_len, BN);
+        if (r.hi > r.lo) {
+            wg_lo = r.lo < wg_lo ? r.lo : wg_lo;
+            wg_hi = r.hi > wg_hi ? r.hi : wg_hi;
+        }
+    }
+    const int h = h_first + (wave % a.hpw);
+    const int s0 = tok_base + (wave / a.hpw) * 32;
+    const int bs = q_len - s0 < 32 ? q_len - s0 : 32;
+    Ranges wr = {0, 0, 0, 0};
+    if (bs > 0) wr = block_ranges(s0, bs, lo_off, hi_off, k_len, BN);
+
+    const uint16_t* kbase = a.k + (int64_t)b * a.kbs + ks.tok0 * a.kts + (int64_t)kvh * a.khs;
+    const uint16_t* vbase = a.v + (int64_t)b * a.vbs + ks.tok0 * a.vts + (int64_t)kvh * a.vhs;
+
+    const int qi = s0 + l32;
+    const bool q_ok = bs > 0 && qi < q_len;
+    s16x8 qop[KD], doop[KD];
+    {
+        const int64_t tokoff = qs.tok0 + qi;
+        const uint16_t* qp = a.q + (int64_t)b * a.qbs + tokoff * a.qts + (int64_t)h * a.qhs;
+        const uint16_t* dop = a.dout + (int64_t)b * a.dobs + tokoff * a.dots + (int64_t)h * a.dohs;
+#pragma unroll
+        for (int kk = 0; kk < KD; ++kk) {
+            s16x8 z = {0, 0, 0, 0, 0, 0, 0, 0};
+            qop[kk] = q_ok ? ld16(qp + 16 * kk + 8 * g) : z;
+            doop[kk] = q_ok ? ld16(dop + 16 * kk + 8 * g) : z;
+        }
+    }
+    float lse_q = INFINITY, del_q = 0.f;
+    if (q_ok) {
+        const int64_t off = (int64_t)h * a.lse_hs + qs.row0 + qi;
+        lse_q = a.lse[off];
+        del_q = a.delta[off];
+    }
+
+    f32x16 acc[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
+
+    KeyTileLoader<D, BN> kl, vl;
+    if (wg_hi > wg_lo) {
+        kl.load(kbase, a.kts, wg_lo, k_len, tid);
+        vl.load(vbase, a.vts, wg_lo, k_len, tid);
+        kl.store(smem[0][0], tid);
+        vl.store(smem[0][1], tid);
+    }
+    int buf = 0;
+    for (int n0 = wg_lo; n0 < wg_hi; n0 += BN) {
+        __syncthreads();
+        const bool more = n0 + BN < wg_hi;
+        if (more) {
+            kl.load(kbase, a.kts, n0 + BN, k_len, tid);
+            vl.load(vbase, a.vts, n0 + BN, k_len, tid);
+        }
+        const bool active = bs > 0 && n0 < wr.hi && n0 + BN > wr.lo;
+        if (active) {
+            const bool masked = !(n0 >= wr.mid_lo && n0 + BN <= wr.mid_hi);
+            const uint16_t* Ks = smem[buf][0];
+            const uint16_t* Vs = smem[buf][1];
+            s16x8 dsb[KB];
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                f32x16 st, dpt;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) st[r] = dpt[r] = 0.f;
+#pragma unroll
+                for (int kk = 0; kk < KD; ++kk) {
+                    st = T::mfma32(lds_row_op<D>(Ks, nb * 32, l32, g, kk), qop[kk], st);
+                    dpt = T::mfma32(lds_row_op<D>(Vs, nb * 32, l32, g, kk), doop[kk], dpt);
+                }
+                float dsv[16];
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    float p = fast_exp2(st[r] * a.qk_scale - lse_q);
+                    if (masked) {
+                        const int key = n0 + nb * 32 + out_row32(r, g);
+                        const int rel = key - qi;
+                        p = (rel >= lo_off && rel <= hi_off && key < k_len) ? p : 0.f;
+                    }
+                    dsv[r] = p * (dpt[r] - del_q);
+                }
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    u32x4 w = {T::pack2(dsv[8 * half], dsv[8 * half + 1]), T::pack2(dsv[8 * half + 2], dsv[8 * half + 3]),
+                               T::pack2(dsv[8 * half + 4], dsv[8 * half + 5]),
+                               T::pack2(dsv[8 * half + 6], dsv[8 * half + 7])};
+                    dsb[nb * 2 + half] = __builtin_bit_cast(s16x8, w);
+                }
+            }
+            // dQ^T += K^T dS^T: A operand K[16 kb + 8 g + i][32 db + l32] by transpose read.
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int kb = 0; kb < KB; ++kb) acc[db] = T::mfma32(lds_tr_op<D>(Ks, db, kb, lane), dsb[kb], acc[db]);
+        }
+        if (more) {
+            kl.store(smem[buf ^ 1][0], tid);
+            vl.store(smem[buf ^ 1][1], tid);
+        }
+        buf ^= 1;
+    }
+
+    if (q_ok) {
+        uint16_t* dqp = a.dq + (int64_t)b * a.dqbs + (qs.tok0 + qi) * a.dqts + (int64_t)h * a.dqhs;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int rq = 0; rq < 4; ++rq) {
+                const int d0 = 32 * db + 8 * rq + 4 * g;
+                if (d0 < D) {
+                    u32x2 w = {T::pack2(acc[db][4 * rq] * a.sm_scale, acc[db][4 * rq + 1] * a.sm_scale),
+                               T::pack2(acc[db][4 * rq + 2] * a.sm_scale, acc[db][4 * rq + 3] * a.sm_scale)};
+                    *reinterpret_cast<u32x2*>(dqp + d0) = w;
+                }
+            }
+    }
+}
+
+int gcd_int(int x, int y) {
+    while (y) {
+        int t = x % y;
+        x = y;
+        y = t;
+    }
+    return x;
+}
+
+BwdArgs make_args(const mykfa_bwd_params& p) {
+    const mykfa_fwd_params& f = p.fwd;
+    BwdArgs a;
+    a.q = static_cast<const uint16_t*>(f.q);
+    a.k = static_cast<const uint16_t*>(f.k);
+    a.v = static_cast<const uint16_t*>(f.v);
+    a.o = static_cast<const uint16_t*>(f.o);
+    a.dout = static_cast<const uint16_t*>(p.dout);
+    a.dq = static_cast<uint16_t*>(p.dq);
+    a.dk = static_cast<uint16_t*>(p.dk);
+    a.dv = static_cast<uint16_t*>(p.dv);
+    a.lse = f.lse;
+    a.delta = p.delta;
+    a.qbs = f.q_batch_stride; a.qts = f.q_token_stride; a.qhs = f.q_head_stride;
+    a.kbs = f.k_batch_stride; a.kts = f.k_token_stride; a.khs = f.k_head_stride;
+    a.vbs = f.v_batch_stride; a.vts = f.v_token_stride; a.vhs = f.v_head_stride;
+    a.obs = f.o_batch_stride; a.ots = f.o_token_stride; a.ohs = f.o_head_stride;
+    a.dobs = p.do_batch_stride; a.dots = p.do_token_stride; a.dohs = p.do_head_stride;
+    a.dqbs = p.dq_batch_stride; a.dqts = p.dq_token_stride; a.dqhs = p.dq_head_stride;
+    a.dkbs = p.dk_batch_stride; a.dkts = p.dk_token_stride; a.dkhs = p.dk_head_stride;
+    a.dvbs = p.dv_batch_stride; a.dvts = p.dv_token_stride; a.dvhs = p.dv_head_stride;
+    a.lse_hs = f.lse_head_stride;
+    a.cu_q = f.cu_seqlens_q;
+    a.cu_k = f.cu_seqlens_k;
+    a.seqlen_q = f.max_seqlen_q;
+    a.seqlen_k = f.max_seqlen_k;
+    a.wl = f.window_left;
+    a.wr = f.window_right;
+    a.qk_scale = f.softmax_scale * 1.4426950408889634f;
+    a.sm_scale = f.softmax_scale;
+    a.group = f.num_heads / f.num_kv_heads;
+    a.hpw = gcd_int(a.group, kWaves);
+    a.num_heads = f.num_heads;
+    a.batch = f.batch;
+    return a;
+}
+
+template <typename T>
+hipError_t preprocess_dtype(const BwdArgs& a, int D, hipStream_t s) {
+    const int rpb = 256 / (D / 8);
+    const long long items = (long long)a.seqlen_q * a.num_heads;
+    dim3 grid((unsigned)((items + rpb - 1) / rpb), a.batch);
+    switch (D) {
+        case 16: hipLaunchKernelGGL((bwd_preprocess_kernel<16, T>), grid, dim3(256), 0, s, a); break;
+        case 32: hipLaunchKernelGGL((bwd_preprocess_kernel<32, T>), grid, dim3(256), 0, s, a); break;
+        case 64: hipLaunchKernelGGL((bwd_preprocess_kernel<64, T>), grid, dim3(256), 0, s, a); break;
+        case 128: hipLaunchKernelGGL((bwd_preprocess_kernel<128, T>), grid, dim3(256), 0, s, a); break;
+        case 256: hipLaunchKernelGGL((bwd_preprocess_kernel<256, T>), grid, dim3(256), 0, s, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t dkdv_dtype(const BwdArgs& a, int D, int num_kv_heads, hipStream_t s) {
+    dim3 grid((a.seqlen_k + 32 * kWaves - 1) / (32 * kWaves), a.batch, num_kv_heads);
+    switch (D) {
+        case 16: hipLaunchKernelGGL((bwd_dkdv_kernel<16, T>), grid, dim3(kThreads), 0, s, a); break;
+        case 32: hipLaunchKernelGGL((bwd_dkdv_kernel<32, T>), grid, dim3(kThreads), 0, s, a); break;
+        case 64: hipLaunchKernelGGL((bwd_dkdv_kernel<64, T>), grid, dim3(kThreads), 0, s, a); break;
+        case 128: hipLaunchKernelGGL((bwd_dkdv_kernel<128, T>), grid, dim3(kThreads), 0, s, a); break;
+        case 256: hipLaunchKernelGGL((bwd_dkdv_kernel<256, T>), grid, dim3(kThreads), 0, s, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t dq_dtype(const BwdArgs& a, int D, hipStream_t s) {
+    const int tpw = kWaves / a.hpw;
+    dim3 grid((a.seqlen_q + tpw * 32 - 1) / (tpw * 32), a.batch, a.num_heads / a.hpw);
+    switch (D) {
+        case 16: hipLaunchKernelGGL((bwd_dq_kernel<16, 64, T>), grid, dim3(kThreads), 0, s, a); break;
+        case 32: hipLaunchKernelGGL((bwd_dq_kernel<32, 64, T>), grid, dim3(kThreads), 0, s, a); break;
+        case 64: hipLaunchKernelGGL((bwd_dq_kernel<64, 64, T>), grid, dim3(kThreads), 0, s, a); break;
+        case 128: hipLaunchKernelGGL((bwd_dq_kernel<128, 64, T>), grid, dim3(kThreads), 0, s, a); break;
+        case 256: hipLaunchKernelGGL((bwd_dq_kernel<256, 32, T>), grid, dim3(kThreads), 0, s, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_bwd_preprocess(const mykfa_bwd_params& p, hipStream_t stream) {
+    BwdArgs a = make_args(p);
+    if (p.fwd.dtype == MYKFA_BF16) return preprocess_dtype<BF16>(a, p.fwd.head_dim, stream);
+    return preprocess_dtype<FP16>(a, p.fwd.head_dim, stream);
+}
+
+hipError_t launch_bwd_dkdv(const mykfa_bwd_params& p, hipStream_t stream) {
+    BwdArgs a = make_args(p);
+    if (p.fwd.dtype == MYKFA_BF16) return dkdv_dtype<BF16>(a, p.fwd.head_dim, p.fwd.num_kv_heads, stream);
+    return dkdv_dtype<FP16>(a, p.fwd.head_dim, p.fwd.num_kv_heads, stream);
+}
+
+hipError_t launch_bwd_dq(const mykfa_bwd_params& p, hipStream_t stream) {
+    BwdArgs a = make_args(p);
+    if (p.fwd.dtype == MYKFA_BF16) return dq_dtype<BF16>(a, p.fwd.head_dim, stream);
+    return dq_dtype<FP16>(a, p.fwd.head_dim, stream);
+}
+
+}  // namespace mykfa

@@ -1,0 +1,193 @@
+// Shared device code for the gfx950 FlashAttention kernels: element types, MFMA
+// wrappers, LDS swizzles, sequence bookkeeping and block-granular tile ranges.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/mykfa.h"
+
+namespace mykfa {
+
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+constexpr float kNegFloor = -1e30f;  // finite row-max floor (flash_attn.py:136-137)
+
+// ---- element types -------------------------------------------------------------------
+
+struct BF16 {
+    static constexpr int code = MYKFA_BF16;
+    __device__ static inline uint16_t from_float(float x) {
+        __bf16 b = (__bf16)x;  // round to nearest even (v_cvt_pk_bf16_f32)
+        return __builtin_bit_cast(uint16_t, b);
+    }
+    __device__ static inline float to_float(uint16_t x) {
+        return __uint_as_float(((uint32_t)x) << 16);
+    }
+    __device__ static inline uint32_t pack2(float a, float b) {
+        return (uint32_t)from_float(a) | ((uint32_t)from_float(b) << 16);
+    }
+    // C(32x32) += A(32x16) * B(16x32); lane l holds A[l%32][8(l/32)+i], B[8(l/32)+i][l%32].
+    __device__ static inline f32x16 mfma32(s16x8 a, s16x8 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    }
+    // C(16x16) += A(16x32) * B(32x16); lane l holds A[l%16][8(l/16)+i], B[8(l/16)+i][l%16].
+    __device__ static inline f32x4 mfma16(s16x8 a, s16x8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    }
+};
+
+struct FP16 {
+    static constexpr int code = MYKFA_FP16;
+    __device__ static inline uint16_t from_float(float x) {
+        _Float16 h = (_Float16)x;
+        return __builtin_bit_cast(uint16_t, h);
+    }
+    __device__ static inline float to_float(uint16_t x) {
+        return (float)__builtin_bit_cast(_Float16, x);
+    }
+    __device__ static inline uint32_t pack2(float a, float b) {
+        return (uint32_t)from_float(a) | ((uint32_t)from_float(b) << 16);
+    }
+    __device__ static inline f32x16 mfma32(s16x8 a, s16x8 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                      __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+    }
+    __device__ static inline f32x4 mfma16(s16x8 a, s16x8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                      __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+    }
+};
+
+// ---- small helpers ---------------------------------------------------------------------
+
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ inline float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+// v_permlane32_swap with both operands x returns, in every lane l, the pair
+// (x[l % 32], x[32 + l % 32]): the values of the two lanes that share a query column of a
+// 32x32 MFMA tile. Combining the pair reduces over that column's two lane groups.
+__device__ inline float max_halves(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float sum_halves(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// 16-byte and 8-byte global accesses.
+__device__ inline s16x8 ld16(const uint16_t* p) { return *reinterpret_cast<const s16x8*>(p); }
+__device__ inline void st16(uint16_t* p, s16x8 v) { *reinterpret_cast<s16x8*>(p) = v; }
+
+// ds_read_b64_tr_b16: within each group of 16 lanes, lane j receives, for i = 0..3, element
+// (j % 4) of the 4-element vector addressed by lane (4 i + j / 4) of its group. When lane
+// s = 4 i + b of the group points at row (r0 + i), column (c0 + 4 b) of a row-major matrix,
+// lane j receives rows r0..r0+3 of column c0 + j: a transposed 4x16 read.
+__device__ inline s16x4 ds_read_tr(const uint16_t* lds_ptr) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds_ptr));
+}
+
+__device__ inline s16x8 cat4(s16x4 a, s16x4 b) {
+    return s16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// ---- LDS layout -----------------------------------------------------------------------
+// Tiles of ROWS x D 16-bit elements live row-major in LDS as 16-byte chunks; chunk c of row
+// r is stored at chunk position c ^ swz(r). swz spreads the rows that one MFMA operand read
+// touches together (rows {0-3, 8-11} and {4-7, 12-15} of every 16, see perm32) over
+// distinct 16-byte bank groups.
+template <int D>
+__device__ inline int lds_swz(int row) {
+    constexpr int CPR = D / 8;  // chunks per row
+    return ((row & 3) | ((row >> 1) & 4)) & (CPR - 1);
+}
+template <int D>
+__device__ inline int lds_off(int row, int col) {  // element offset of (row, col)
+    return row * D + ((((col >> 3) ^ lds_swz<D>(row))) << 3) + (col & 7);
+}
+
+// Row permutation used when a 32-row tile is the A operand of a 32x32x16 MFMA whose output
+// then feeds another MFMA as its k-operand: swapping rows 4-7 with 8-11 (in each 16) makes
+// output register r of lane group g hold row 16 (r / 8) + 8 g + r % 8, i.e. each lane
+// group holds 8 consecutive rows per 16, the k-slot order of the next MFMA.
+__device__ inline int perm32(int rho) { return (rho & ~12) | ((rho & 4) << 1) | ((rho & 8) >> 1); }
+// Tile row held by output register r (0..15) of lane group g after the permuted load.
+__device__ inline int out_row32(int r, int g) { return 16 * (r >> 3) + 8 * g + (r & 7); }
+
+// ---- sequences --------------------------------------------------------------------------
+
+struct SeqInfo {
+    int64_t tok0;  // first token of the sequence in the (packed) tensor
+    int64_t row0;  // first row in the (heads, rows) lse/delta buffers
+    int len;
+};
+
+// flash_attn.py:39-55 (_seq_info).
+__device__ inline SeqInfo seq_info(int b, const int32_t* cu, const int32_t* seqused, int seqlen,
+                                   bool use_seqused) {
+    SeqInfo s;
+    if (cu != nullptr) {
+        int start = cu[b];
+        s.len = cu[b + 1] - start;
+        s.tok0 = start;
+        s.row0 = start;
+    } else {
+        s.tok0 = 0;
+        s.row0 = (int64_t)b * seqlen;
+        int len = seqlen;
+        if (use_seqused && seqused != nullptr) {  // clamp: never read beyond the cache capacity
+            len = seqused[b];
+            len = len < 0 ? 0 : (len > seqlen ? seqlen : len);
+        }
+        s.len = len;
+    }
+    return s;
+}
+
+// Block ranges, flash_attn.py:58-68 (_block_ranges). For "self" indices [s0, s0 + BS),
+// each seeing "other" indices t with lo_off <= t - s <= hi_off and 0 <= t < t_len, the
+// BT-aligned range [lo, hi) of t to visit, split as [lo, mid_lo) masked,
+// [mid_lo, mid_hi) unmasked for every s, [mid_hi, hi) masked.
+struct Ranges {
+    int lo, mid_lo, mid_hi, hi;
+};
+__host__ __device__ inline Ranges block_ranges(int s0, int BS, int lo_off, int hi_off, int t_len, int BT) {
+    Ranges r;
+    int a = s0 + lo_off;
+    r.lo = (a > 0 ? a : 0) / BT * BT;
+    int h = s0 + BS + hi_off;
+    h = h < t_len ? h : t_len;
+    r.hi = h > r.lo ? h : r.lo;
+    int m = s0 + BS - 1 + lo_off;
+    m = m > r.lo ? m : r.lo;
+    int ml = (m + BT - 1) / BT * BT;  // m >= lo >= 0
+    r.mid_lo = ml < r.hi ? ml : r.hi;
+    int mh = s0 + hi_off + 1;
+    mh = mh < t_len ? mh : t_len;
+    mh = mh > 0 ? mh : 0;
+    mh = mh / BT * BT;
+    r.mid_hi = mh > r.mid_lo ? mh : r.mid_lo;
+    return r;
+}
+
+// Offsets of windowed causal masking: query i sees key j iff lo_off <= j - i <= hi_off.
+__device__ inline int band_lo(int k_len, int q_len, int wl) { return k_len - q_len - wl; }
+__device__ inline int band_hi(int k_len, int q_len, int wr) {
+    // wr may be 2^30: keep the sum within int32
+    long long v = (long long)k_len - q_len + wr;
+    return v > (1 << 30) ? (1 << 30) : (int)v;
+}
+
+}  // namespace mykfa

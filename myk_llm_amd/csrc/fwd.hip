@@ -1,0 +1,323 @@
+// Prefill forward: O and base-2 LSE (replaces _fwd_kernel, flash_attn.py:106-154).
+//
+// Work decomposition. A workgroup is 4 waves; every wave owns 32 query rows of one head.
+// The workgroup's waves cover `hpw` query heads of ONE GQA group (hpw = gcd(group, 4)) times
+// 4 / hpw blocks of 32 consecutive tokens, so each K/V tile staged in LDS serves every
+// query head of the group that the workgroup holds: K/V bytes are fetched once per group.
+//
+// Per 64-key tile, each wave computes S^T = K Q^T on 32x32x16 bf16 MFMA (K from LDS as the
+// A operand, Q resident in registers as the B operand), so that the output lane of every
+// score is its query and the registers are keys. The online softmax (row max through a
+// permlane32 swap, exp2 on the fp32 scores) then produces P^T already in the k-operand
+// layout of the next product O^T += V^T P^T, whose A operand (V^T) is read straight from
+// the row-major V tile with the gfx950 LDS transpose read. K/V tiles are double-buffered in
+// LDS with an XOR chunk swizzle. Key tiles wholly outside a wave's causal/window band are
+// skipped, and only tiles that cross the band edge evaluate the element mask (the 3-range
+// split of flash_attn.py:140-145).
+#include "common.h"
+#include "kernels.h"
+
+namespace mykfa {
+
+namespace {
+
+struct FwdArgs {
+    const uint16_t* q;
+    const uint16_t* k;
+    const uint16_t* v;
+    uint16_t* o;
+    float* lse;
+    int64_t qbs, qts, qhs, kbs, kts, khs, vbs, vts, vhs, obs, ots, ohs, lse_hs;
+    const int32_t* cu_q;
+    const int32_t* cu_k;
+    const int32_t* seqused_k;
+    int seqlen_q, seqlen_k;
+    int wl, wr;
+    float qk_scale;  // softmax_scale * log2(e)  (flash_attn.py:368)
+    int group;       // num_heads / num_kv_heads
+    int hpw;         // query heads per workgroup
+};
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+
+// Stage a BN x D tile (rows n0.., masked to < len) from global into a swizzled LDS tile.
+template <int D, int BN>
+struct TileLoader {
+    static constexpr int CPR = D / 8;
+    static constexpr int CHUNKS = BN * CPR;
+    static constexpr int PER = (CHUNKS + kThreads - 1) / kThreads;
+    s16x8 r[PER];
+
+    __device__ inline void load(const uint16_t* base, int64_t tstride, int n0, int len, int tid) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            int idx = tid + i * kThreads;
+            int row = idx / CPR, ch = idx % CPR;
+            s16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
+            if ((CHUNKS % kThreads == 0 || idx < CHUNKS) && n0 + row < len)
+                v = ld16(base + (int64_t)(n0 + row) * tstride + ch * 8);
+            r[i] = v;
+        }
+    }
+    __device__ inline void store(uint16_t* lds, int tid) const {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            int idx = tid + i * kThreads;
+            if (CHUNKS % kThreads == 0 || idx < CHUNKS) {
+                int row = idx / CPR, ch = idx % CPR;
+                *reinterpret_cast<s16x8*>(lds + row * D + ((ch ^ lds_swz<D>(row)) << 3)) = r[i];
+            }
+        }
+    }
+};
+
+template <int D, int BN, typename T>
+__global__ __launch_bounds__(kThreads) void fwd_kernel(FwdArgs a) {
+    constexpr int KD = D / 16;            // k-steps of S^T = K Q^T
+    constexpr int DB = (D + 31) / 32;     // 32-row blocks of O^T
+    constexpr int NB = BN / 32;           // 32-key blocks per tile
+    constexpr int KB = BN / 16;           // 16-key k-steps of O^T += V^T P^T
+    __shared__ __attribute__((aligned(16))) uint16_t smem[2][2][BN * D];
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int l32 = lane & 31, g = lane >> 5;
+    const int tpw = kWaves / a.hpw;
+    const int mblk = gridDim.x - 1 - blockIdx.x;  // longest causal rows first (flash_attn.py:115)
+    const int b = blockIdx.y;
+    const int h_first = blockIdx.z * a.hpw;
+
+    SeqInfo qs = seq_info(b, a.cu_q, nullptr, a.seqlen_q, false);
+    const int tok_base = mblk * tpw * 32;
+    if (tok_base >= qs.len) return;
+    SeqInfo ks = seq_info(b, a.cu_k, a.seqused_k, a.seqlen_k, true);
+    const int q_len = qs.len, k_len = ks.len;
+    const int kvh = h_first / a.group;
+    const int lo_off = band_lo(k_len, q_len, a.wl);
+    const int hi_off = band_hi(k_len, q_len, a.wr);
+
+    // Key range of the workgroup: union over its token blocks.
+    int wg_lo = 1 << 30, wg_hi = 0;
+    for (int tb = 0; tb < tpw; ++tb) {
+        int s0 = tok_base + tb * 32;
+        int bs = q_len - s0 < 32 ? q_len - s0 : 32;
+        if (bs <= 0) continue;
+        Ranges r = block_ranges(s0, bs, lo_off, hi_off, k_len, BN);
+        if (r.hi > r.lo) {
+            wg_lo = r.lo < wg_lo ? r.lo : wg_lo;
+            wg_hi = r.hi > wg_hi ? r.hi : wg_hi;
+        }
+    }
+
+    const int h = h_first + (wave % a.hpw);
+    const int s0 = tok_base + (wave / a.hpw) * 32;
+    const int bs = q_len - s0 < 32 ? q_len - s0 : 32;
+    Ranges wr = {0, 0, 0, 0};
+    if (bs > 0) wr = block_ranges(s0, bs, lo_off, hi_off, k_len, BN);
+
+    const uint16_t* kbase = a.k + (int64_t)b * a.kbs + ks.tok0 * a.kts + (int64_t)kvh * a.khs;
+    const uint16_t* vbase = a.v + (int64_t)b * a.vbs + ks.tok0 * a.vts + (int64_t)kvh * a.vhs;
+
+    // Q rows of this wave as the B operand of S^T = K Q^T: lane holds Q[s0 + l32][16kk + 8g + i].
+    s16x8 qop[KD];
+    {
+        const int qi = s0 + l32;
+        const uint16_t* qp = a.q + (int64_t)b * a.qbs + (qs.tok0 + qi) * a.qts + (int64_t)h * a.qhs;
+#pragma unroll
+        for (int kk = 0; kk < KD; ++kk) {
+            s16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
+            if (qi < q_len) v = ld16(qp + 16 * kk + 8 * g);
+            qop[kk] = v;
+        }
+    }
+
+    f32x16 acc[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
+    float m_i = kNegFloor, l_i = 0.f;
+    const int qi = s0 + l32;
+
+    TileLoader<D, BN> kl, vl;
+    if (wg_hi > wg_lo) {
+        kl.load(kbase, a.kts, wg_lo, k_len, tid);
+        vl.load(vbase, a.vts, wg_lo, k_len, tid);
+        kl.store(smem[0][0], tid);
+        vl.store(smem[0][1], tid);
+    }
+    int buf = 0;
+    for (int n0 = wg_lo; n0 < wg_hi; n0 += BN) {
+        __syncthreads();
+        const bool more = n0 + BN < wg_hi;
+        if (more) {
+            kl.load(kbase, a.kts, n0 + BN, k_len, tid);
+            vl.load(vbase, a.vts, n0 + BN, k_len, tid);
+        }
+        const bool active = bs > 0 && n0 < wr.hi && n0 + BN > wr.lo;
+        if (active) {
+            const bool masked = !(n0 >= wr.mid_lo && n0 + BN <= wr.mid_hi);
+            const uint16_t* Ks = smem[buf][0];
+            const uint16_t* Vs = smem[buf][1];
+            // S^T = K Q^T, 32 keys per block.
+            f32x16 st[NB];
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) st[nb][r] = 0.f;
+                const int row = nb * 32 + perm32(l32);
+#pragma unroll
+                for (int kk = 0; kk < KD; ++kk) {
+                    s16x8 kop = *reinterpret_cast<const s16x8*>(Ks + row * D + (((2 * kk + g) ^ lds_swz<D>(row)) << 3));
+                    st[nb] = T::mfma32(kop, qop[kk], st[nb]);
+                }
+            }
+            // Online softmax (flash_attn.py:90-96) on scaled scores.
+            float mx = kNegFloor;
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    float x = st[nb][r] * a.qk_scale;
+                    if (masked) {
+                        const int key = n0 + nb * 32 + out_row32(r, g);
+                        const int rel = key - qi;
+                        const bool vis = rel >= lo_off && rel <= hi_off && key < k_len;
+                        x = vis ? x : -INFINITY;
+                    }
+                    st[nb][r] = x;
+                    mx = fmaxf(mx, x);
+                }
+            mx = max_halves(mx);
+            const float m_new = fmaxf(m_i, mx);
+            const float alpha = fast_exp2(m_i - m_new);
+            float lsum = 0.f;
+            s16x8 pop[KB];
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    uint32_t w[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        float p0 = fast_exp2(st[nb][8 * half + 2 * i] - m_new);
+                        float p1 = fast_exp2(st[nb][8 * half + 2 * i + 1] - m_new);
+                        lsum += p0 + p1;
+                        w[i] = T::pack2(p0, p1);
+                    }
+                    u32x4 wv = {w[0], w[1], w[2], w[3]};
+                    pop[nb * 2 + half] = __builtin_bit_cast(s16x8, wv);
+                }
+            l_i = l_i * alpha + lsum;
+            m_i = m_new;
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
+            // O^T += V^T P^T; V^T operand through the LDS transpose read.
+            const int G = lane >> 4, jj = lane & 15;
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+                int col = 32 * db + 16 * (G & 1) + 4 * (jj & 3);
+                const bool dvalid = col < D;
+                if (!dvalid) col = col % D;
+#pragma unroll
+                for (int kb = 0; kb < KB; ++kb) {
+                    const int row = 16 * kb + 8 * (G >> 1) + (jj >> 2);
+                    s16x4 lo4 = ds_read_tr(Vs + lds_off<D>(row, col));
+                    s16x4 hi4 = ds_read_tr(Vs + lds_off<D>(row + 4, col));
+                    s16x8 vop = cat4(lo4, hi4);
+                    if (!dvalid) vop = s16x8{0, 0, 0, 0, 0, 0, 0, 0};
+                    acc[db] = T::mfma32(vop, pop[kb], acc[db]);
+                }
+            }
+        }
+        if (more) {
+            kl.store(smem[buf ^ 1][0], tid);
+            vl.store(smem[buf ^ 1][1], tid);
+        }
+        buf ^= 1;
+    }
+
+    if (bs <= 0) return;
+    // Epilogue (flash_attn.py:147-154): rows that saw no key output 0 and lse = +inf.
+    const float l_tot = sum_halves(l_i);
+    const bool empty = l_tot == 0.f;
+    const float inv = empty ? 0.f : 1.f / l_tot;
+    if (qi < q_len) {
+        uint16_t* op = a.o + (int64_t)b * a.obs + (qs.tok0 + qi) * a.ots + (int64_t)h * a.ohs;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int rq = 0; rq < 4; ++rq) {
+                const int d0 = 32 * db + 8 * rq + 4 * g;
+                if (d0 < D) {
+                    u32x2 w = {T::pack2(acc[db][4 * rq] * inv, acc[db][4 * rq + 1] * inv),
+                               T::pack2(acc[db][4 * rq + 2] * inv, acc[db][4 * rq + 3] * inv)};
+                    *reinterpret_cast<u32x2*>(op + d0) = w;
+                }
+            }
+        if (g == 0) a.lse[(int64_t)h * a.lse_hs + qs.row0 + qi] = empty ? INFINITY : m_i + fast_log2(l_tot);
+    }
+}
+
+int gcd_int(int x, int y) {
+    while (y) {
+        int t = x % y;
+        x = y;
+        y = t;
+    }
+    return x;
+}
+
+template <int D, int BN, typename T>
+hipError_t launch_typed(const FwdArgs& args, int batch, int num_heads, int max_q, hipStream_t s) {
+    const int tpw = kWaves / args.hpw;
+    dim3 grid((max_q + tpw * 32 - 1) / (tpw * 32), batch, num_heads / args.hpw);
+    if (grid.x == 0 || batch == 0) return hipSuccess;
+    hipLaunchKernelGGL((fwd_kernel<D, BN, T>), grid, dim3(kThreads), 0, s, args);
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_dtype(const FwdArgs& args, int D, int batch, int num_heads, int max_q, hipStream_t s) {
+    switch (D) {
+        case 16: return launch_typed<16, 64, T>(args, batch, num_heads, max_q, s);
+        case 32: return launch_typed<32, 64, T>(args, batch, num_heads, max_q, s);
+        case 64: return launch_typed<64, 64, T>(args, batch, num_heads, max_q, s);
+        case 128: return launch_typed<128, 64, T>(args, batch, num_heads, max_q, s);
+        case 256: return launch_typed<256, 32, T>(args, batch, num_heads, max_q, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_fwd(const mykfa_fwd_params& p, hipStream_t stream) {
+    FwdArgs a;
+    a.q = static_cast<const uint16_t*>(p.q);
+    a.k = static_cast<const uint16_t*>(p.k);
+    a.v = static_cast<const uint16_t*>(p.v);
+    a.o = static_cast<uint16_t*>(p.o);
+    a.lse = p.lse;
+    a.qbs = p.q_batch_stride; a.qts = p.q_token_stride; a.qhs = p.q_head_stride;
+    a.kbs = p.k_batch_stride; a.kts = p.k_token_stride; a.khs = p.k_head_stride;
+    a.vbs = p.v_batch_stride; a.vts = p.v_token_stride; a.vhs = p.v_head_stride;
+    a.obs = p.o_batch_stride; a.ots = p.o_token_stride; a.ohs = p.o_head_stride;
+    a.lse_hs = p.lse_head_stride;
+    a.cu_q = p.cu_seqlens_q;
+    a.cu_k = p.cu_seqlens_k;
+    a.seqused_k = p.seqused_k;
+    a.seqlen_q = p.max_seqlen_q;
+    a.seqlen_k = p.max_seqlen_k;
+    a.wl = p.window_left;
+    a.wr = p.window_right;
+    a.qk_scale = p.softmax_scale * 1.4426950408889634f;
+    a.group = p.num_heads / p.num_kv_heads;
+    a.hpw = gcd_int(a.group, kWaves);
+    if (p.dtype == MYKFA_BF16) return launch_dtype<BF16>(a, p.head_dim, p.batch, p.num_heads, p.max_seqlen_q, stream);
+    return launch_dtype<FP16>(a, p.head_dim, p.batch, p.num_heads, p.max_seqlen_q, stream);
+}
+
+}  // namespace mykfa

@@ -1,0 +1,27 @@
+// Host-side launchers of the gfx950 kernels (one translation unit per kernel family).
+// Each returns the HIP status of its launch; argument checking happens in api.hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "../../include/mykfa.h"
+
+namespace mykfa {
+
+hipError_t launch_fwd(const mykfa_fwd_params& p, hipStream_t stream);
+
+hipError_t launch_bwd_preprocess(const mykfa_bwd_params& p, hipStream_t stream);
+hipError_t launch_bwd_dkdv(const mykfa_bwd_params& p, hipStream_t stream);
+hipError_t launch_bwd_dq(const mykfa_bwd_params& p, hipStream_t stream);
+
+// Split-K decode. The workspace holds, per (split, batch, head, query): D fp32 partial
+// outputs, then one fp32 partial lse per (split, batch, head, query).
+size_t decode_workspace_bytes(int batch, int num_heads, int seqlen_q, int head_dim, int num_splits);
+int decode_default_splits(int batch, int num_kv_heads, int capacity);
+hipError_t launch_decode_splitk(const mykfa_decode_params& p, int num_splits, void* ws, hipStream_t stream);
+hipError_t launch_decode_merge(const mykfa_decode_params& p, int num_splits, const void* ws,
+                               hipStream_t stream);
+
+hipError_t launch_kv_append(const mykfa_kv_append_params& p, hipStream_t stream);
+
+}  // namespace mykfa

@@ -1,0 +1,356 @@
+"""FlashAttention on MI355X (gfx950): the host side of the drop-in for myk-llm's
+src/myk_llm/ops/flash_attn.py.
+
+The three public functions keep the reference's names, signatures, defaults and exception
+types (flash_attn.py:442-490), so model code calls them unchanged:
+
+    flash_attn_func          (batch, seq, heads, head_dim) tensors
+    flash_attn_varlen_func   packed (tokens, heads, head_dim) documents with cu_seqlens
+    flash_attn_with_kvcache  writes new keys/values into a static cache, then attends
+                             (forward only; capturable in a HIP graph)
+
+Each also takes a keyword-only ``return_softmax_lse=False``; when True it returns
+``(out, lse)`` where lse is the fp32 base-2 log-sum-exp laid out ``(heads, rows)``, the
+buffer the reference's ``_forward`` produces (flash_attn.py:353-373).
+
+Semantics (flash_attn.py:11-18): causal or bidirectional attention, a sliding window, GQA,
+bf16/fp16 inputs, head_dim in {16, 32, 64, 128, 256}; queries are aligned to the END of the
+keys: query i of Lq sits at key position i + Lk - Lq and sees keys j with
+``i + Lk - Lq - window_left <= j <= i + Lk - Lq + window_right``, a side of -1 being
+unbounded and causal forcing window_right = 0.
+
+All arithmetic runs in the hand-written gfx950 kernels of libmykfa.so, called through its C
+ABI (include/mykfa.h) on torch's current stream. Python only validates, allocates outputs
+with torch's caching allocator and passes pointers. There is no CPU or PyTorch fallback:
+without the library every call raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Optional
+
+import torch
+from torch import Tensor
+
+from . import _lib
+
+_UNBOUNDED = _lib.UNBOUNDED  # flash_attn.py:32
+_HEAD_DIMS = (16, 32, 64, 128, 256)  # flash_attn.py:322-323
+_DECODE_MAX_Q = 16  # few queries per sequence use the split-K decode kernel (flash_attn.py:364)
+
+
+# --- validation (flash_attn.py:331-350) ---------------------------------------------------
+
+
+def _check_meta(q: Tensor, k: Tensor, v: Tensor) -> None:
+    """dtype / head_dim / head-ratio checks of _check (flash_attn.py:340-346)."""
+    head_dim = q.shape[-1]
+    if q.dtype not in (torch.bfloat16, torch.float16) or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise TypeError(f"flash attention needs matching bf16/fp16 q, k, v; got {q.dtype}, {k.dtype}, {v.dtype}")
+    if head_dim not in _HEAD_DIMS or k.shape[-1] != head_dim or v.shape[-1] != head_dim:
+        raise ValueError(f"head_dim must be one of {list(_HEAD_DIMS)} for q, k and v; got "
+                         f"{q.shape[-1]}, {k.shape[-1]}, {v.shape[-1]}")
+    if q.shape[-2] % k.shape[-2] or k.shape[-2] != v.shape[-2]:
+        raise ValueError(f"query heads ({q.shape[-2]}) must be a multiple of key/value heads ({k.shape[-2]})")
+
+
+def _check(q: Tensor, k: Tensor, v: Tensor) -> None:
+    """flash_attn.py:336-346, same order and exception types."""
+    if not (q.is_cuda and k.is_cuda and v.is_cuda):
+        raise RuntimeError("flash attention is CUDA-only: q, k and v must be GPU (HIP) tensors")
+    _check_meta(q, k, v)
+
+
+def _last_dim_contiguous(x: Tensor) -> Tensor:
+    return x if x.stride(-1) == 1 else x.contiguous()
+
+
+def _strides(x: Tensor) -> tuple[int, int, int]:
+    """(batch, token, head) strides in elements; batch is 0 for packed varlen tensors."""
+    return (x.stride(0), x.stride(1), x.stride(2)) if x.dim() == 4 else (0, x.stride(0), x.stride(1))
+
+
+def _kernel_ready(x: Tensor) -> Tensor:
+    """The kernels read 16 bytes at a time along head_dim: a 16-byte aligned base and
+    strides that are multiples of 8 elements. Anything else is copied once."""
+    if x.stride(-1) == 1 and x.data_ptr() % 16 == 0 and all(s % 8 == 0 for s in x.stride()[:-1]):
+        return x
+    return x.contiguous()
+
+
+def _window(causal: bool, window_size: tuple[int, int]) -> tuple[int, int]:
+    """flash_attn.py:435-439."""
+    left, right = window_size
+    left = _UNBOUNDED if left < 0 else left
+    right = 0 if causal else (_UNBOUNDED if right < 0 else right)
+    return left, right
+
+
+def _dtype_code(dtype: torch.dtype) -> int:
+    return _lib.DTYPE_BF16 if dtype == torch.bfloat16 else _lib.DTYPE_FP16
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _ptr(x: Optional[Tensor]) -> Optional[int]:
+    return None if x is None else x.data_ptr()
+
+
+class _DeviceGuard:
+    """Makes x's device current for the launch when it is not already."""
+
+    def __init__(self, device: torch.device):
+        self.device = device
+        self.guard = None
+
+    def __enter__(self):
+        if self.device.index is not None and self.device.index != torch.cuda.current_device():
+            self.guard = torch.cuda.device(self.device)
+            self.guard.__enter__()
+
+    def __exit__(self, *exc):
+        if self.guard is not None:
+            self.guard.__exit__(*exc)
+
+
+def _fwd_params(q, k, v, out, lse, cu_q, cu_k, seqused_k, max_q, max_k, scale, wl, wr) -> _lib.FwdParams:
+    varlen = cu_q is not None
+    p = _lib.FwdParams()
+    p.q, p.k, p.v, p.o, p.lse = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr()
+    p.q_batch_stride, p.q_token_stride, p.q_head_stride = _strides(q)
+    p.k_batch_stride, p.k_token_stride, p.k_head_stride = _strides(k)
+    p.v_batch_stride, p.v_token_stride, p.v_head_stride = _strides(v)
+    p.o_batch_stride, p.o_token_stride, p.o_head_stride = _strides(out)
+    p.lse_head_stride = lse.stride(0)
+    p.cu_seqlens_q, p.cu_seqlens_k, p.seqused_k = _ptr(cu_q), _ptr(cu_k), _ptr(seqused_k)
+    p.batch = cu_q.numel() - 1 if varlen else q.shape[0]
+    p.num_heads, p.num_kv_heads, p.head_dim = q.shape[-2], k.shape[-2], q.shape[-1]
+    p.max_seqlen_q, p.max_seqlen_k = max_q, max_k
+    p.window_left, p.window_right = wl, wr
+    p.softmax_scale = scale
+    p.dtype = _dtype_code(q.dtype)
+    return p
+
+
+def _int32(x: Optional[Tensor]) -> Optional[Tensor]:
+    if x is None:
+        return None
+    return x if (x.dtype == torch.int32 and x.is_contiguous()) else x.to(torch.int32).contiguous()
+
+
+# --- launchers (flash_attn.py:353-406) ----------------------------------------------------
+
+
+def _forward(q: Tensor, k: Tensor, v: Tensor, cu_seqlens_q: Optional[Tensor], cu_seqlens_k: Optional[Tensor],
+             seqused_k: Optional[Tensor], max_seqlen_q: int, max_seqlen_k: int, softmax_scale: float,
+             window_left: int, window_right: int) -> tuple[Tensor, Tensor]:
+    """O and the base-2 LSE (num_heads, rows), fp32 (flash_attn.py:353-373)."""
+    varlen = cu_seqlens_q is not None
+    q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
+    cu_q, cu_k, seqused = _int32(cu_seqlens_q), _int32(cu_seqlens_k), _int32(seqused_k)
+    rows = q.shape[0] if varlen else q.shape[0] * q.shape[1]
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    lse = torch.empty((q.shape[-2], rows), dtype=torch.float32, device=q.device)
+    p = _fwd_params(q, k, v, out, lse, cu_q, cu_k, seqused, max_seqlen_q, max_seqlen_k, softmax_scale,
+                    window_left, window_right)
+    L = _lib.lib()
+    with _DeviceGuard(q.device):
+        if not varlen and 0 < max_seqlen_q <= _DECODE_MAX_Q:
+            _decode_launch(L, p, q.device)
+        else:
+            _lib.check(L.mykfa_fwd(ctypes.byref(p), _stream(q.device)))
+    return out, lse
+
+
+def _decode_launch(L, p: _lib.FwdParams, device: torch.device) -> None:
+    """Split-K decode with its LSE merge; the workspace comes from torch's allocator."""
+    d = _lib.DecodeParams()
+    d.fwd = p
+    d.num_splits = 0
+    splits = L.mykfa_decode_num_splits(p.batch, p.num_kv_heads, p.max_seqlen_k)
+    d.num_splits = splits
+    nbytes = L.mykfa_decode_workspace_size(p.batch, p.num_heads, p.max_seqlen_q, p.head_dim, splits)
+    ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=device)
+    _lib.check(L.mykfa_decode(ctypes.byref(d), ws.data_ptr(), ws.numel(), _stream(device)))
+
+
+def _backward(dout: Tensor, q: Tensor, k: Tensor, v: Tensor, out: Tensor, lse: Tensor,
+              cu_seqlens_q: Optional[Tensor], cu_seqlens_k: Optional[Tensor], max_seqlen_q: int,
+              max_seqlen_k: int, softmax_scale: float, window_left: int,
+              window_right: int) -> tuple[Tensor, Tensor, Tensor]:
+    """dQ, dK, dV (flash_attn.py:376-406)."""
+    dout = _kernel_ready(dout)
+    q, k, v, out = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v), _kernel_ready(out)
+    cu_q, cu_k = _int32(cu_seqlens_q), _int32(cu_seqlens_k)
+    dq = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    dk = torch.empty(k.shape, dtype=k.dtype, device=k.device)
+    dv = torch.empty(v.shape, dtype=v.dtype, device=v.device)
+    delta = torch.empty_like(lse)
+    p = _lib.BwdParams()
+    p.fwd = _fwd_params(q, k, v, out, lse, cu_q, cu_k, None, max_seqlen_q, max_seqlen_k, softmax_scale,
+                        window_left, window_right)
+    p.dout, p.dq, p.dk, p.dv, p.delta = dout.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), delta.data_ptr()
+    p.do_batch_stride, p.do_token_stride, p.do_head_stride = _strides(dout)
+    p.dq_batch_stride, p.dq_token_stride, p.dq_head_stride = _strides(dq)
+    p.dk_batch_stride, p.dk_token_stride, p.dk_head_stride = _strides(dk)
+    p.dv_batch_stride, p.dv_token_stride, p.dv_head_stride = _strides(dv)
+    L = _lib.lib()
+    with _DeviceGuard(q.device):
+        _lib.check(L.mykfa_bwd(ctypes.byref(p), _stream(q.device)))
+    return dq, dk, dv
+
+
+def _kv_append(k_cache: Tensor, v_cache: Tensor, k: Tensor, v: Tensor, cache_seqlens: Tensor) -> None:
+    """cache[b, cache_seqlens[b] + t] = new[b, t] (flash_attn.py:480-485)."""
+    k, v = _kernel_ready(k), _kernel_ready(v)
+    seqlens = _int32(cache_seqlens)
+    p = _lib.KvAppendParams()
+    p.k_cache, p.v_cache, p.k_new, p.v_new = k_cache.data_ptr(), v_cache.data_ptr(), k.data_ptr(), v.data_ptr()
+    p.cache_seqlens = seqlens.data_ptr()
+    p.kc_batch_stride, p.kc_token_stride, p.kc_head_stride = _strides(k_cache)
+    p.vc_batch_stride, p.vc_token_stride, p.vc_head_stride = _strides(v_cache)
+    p.kn_batch_stride, p.kn_token_stride, p.kn_head_stride = _strides(k)
+    p.vn_batch_stride, p.vn_token_stride, p.vn_head_stride = _strides(v)
+    p.batch, p.seqlen_new, p.capacity = k.shape[0], k.shape[1], k_cache.shape[1]
+    p.num_kv_heads, p.head_dim, p.dtype = k.shape[2], k.shape[3], _dtype_code(k.dtype)
+    L = _lib.lib()
+    with _DeviceGuard(k_cache.device):
+        _lib.check(L.mykfa_kv_append(ctypes.byref(p), _stream(k_cache.device)))
+
+
+# --- torch.library ops: opaque to torch.compile, so fullgraph tracing needs no break ------
+
+
+@torch.library.custom_op("mykfa::fwd", mutates_args=())
+def _fwd_op(q: Tensor, k: Tensor, v: Tensor, cu_seqlens_q: Optional[Tensor], cu_seqlens_k: Optional[Tensor],
+            seqused_k: Optional[Tensor], max_seqlen_q: int, max_seqlen_k: int, softmax_scale: float,
+            window_left: int, window_right: int) -> tuple[Tensor, Tensor]:
+    return _forward(q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k, max_seqlen_q, max_seqlen_k, softmax_scale,
+                    window_left, window_right)
+
+
+@_fwd_op.register_fake
+def _(q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_k, max_seqlen_q, max_seqlen_k, softmax_scale, window_left,
+      window_right):
+    rows = q.shape[0] if cu_seqlens_q is not None else q.shape[0] * q.shape[1]
+    return torch.empty_like(q, memory_format=torch.contiguous_format), q.new_empty((q.shape[-2], rows),
+                                                                                   dtype=torch.float32)
+
+
+@torch.library.custom_op("mykfa::bwd", mutates_args=())
+def _bwd_op(dout: Tensor, q: Tensor, k: Tensor, v: Tensor, out: Tensor, lse: Tensor,
+            cu_seqlens_q: Optional[Tensor], cu_seqlens_k: Optional[Tensor], max_seqlen_q: int, max_seqlen_k: int,
+            softmax_scale: float, window_left: int, window_right: int) -> tuple[Tensor, Tensor, Tensor]:
+    return _backward(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+                     softmax_scale, window_left, window_right)
+
+
+@_bwd_op.register_fake
+def _(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale,
+      window_left, window_right):
+    fmt = torch.contiguous_format
+    return (torch.empty_like(q, memory_format=fmt), torch.empty_like(k, memory_format=fmt),
+            torch.empty_like(v, memory_format=fmt))
+
+
+@torch.library.custom_op("mykfa::kv_append", mutates_args=("k_cache", "v_cache"))
+def _kv_append_op(k_cache: Tensor, v_cache: Tensor, k: Tensor, v: Tensor, cache_seqlens: Tensor) -> None:
+    _kv_append(k_cache, v_cache, k, v, cache_seqlens)
+
+
+@_kv_append_op.register_fake
+def _(k_cache, v_cache, k, v, cache_seqlens):
+    return None
+
+
+def _compiling() -> bool:
+    return torch.compiler.is_compiling()
+
+
+def _fwd(*args):
+    return _fwd_op(*args) if _compiling() else _forward(*args)
+
+
+def _bwd(*args):
+    return _bwd_op(*args) if _compiling() else _backward(*args)
+
+
+# --- autograd (flash_attn.py:412-429) ------------------------------------------------------
+
+
+class _FlashAttn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale,
+                window_left, window_right):
+        out, lse = _fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, None, max_seqlen_q, max_seqlen_k, softmax_scale,
+                        window_left, window_right)
+        ctx.save_for_backward(q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k)
+        ctx.args = (max_seqlen_q, max_seqlen_k, softmax_scale, window_left, window_right)
+        ctx.mark_non_differentiable(lse)
+        return out, lse
+
+    @staticmethod
+    def backward(ctx, dout, dlse):  # pyright: ignore[reportIncompatibleMethodOverride]
+        q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k = ctx.saved_tensors
+        dq, dk, dv = _bwd(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, *ctx.args)
+        return dq, dk, dv, None, None, None, None, None, None, None
+
+
+# --- public API (flash_attn.py:442-490) ----------------------------------------------------
+
+
+def flash_attn_func(
+    q: Tensor, k: Tensor, v: Tensor, causal: bool = False, window_size: tuple[int, int] = (-1, -1),
+    softmax_scale: float | None = None, *, return_softmax_lse: bool = False,
+):
+    """q (batch, seqlen_q, heads, head_dim), k/v (batch, seqlen_k, kv_heads, head_dim)."""
+    _check(q, k, v)
+    q, k, v = (_last_dim_contiguous(x) for x in (q, k, v))
+    scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(q.shape[-1])
+    out, lse = _FlashAttn.apply(q, k, v, None, None, q.shape[1], k.shape[1], scale, *_window(causal, window_size))
+    return (out, lse) if return_softmax_lse else out
+
+
+def flash_attn_varlen_func(
+    q: Tensor, k: Tensor, v: Tensor, cu_seqlens_q: Tensor, cu_seqlens_k: Tensor, max_seqlen_q: int,
+    max_seqlen_k: int, causal: bool = False, window_size: tuple[int, int] = (-1, -1),
+    softmax_scale: float | None = None, *, return_softmax_lse: bool = False,
+):
+    """Packed q (total_q, heads, head_dim), k/v (total_k, kv_heads, head_dim); sequence b
+    spans rows cu_seqlens[b]:cu_seqlens[b + 1] (int32)."""
+    _check(q, k, v)
+    q, k, v = (_last_dim_contiguous(x) for x in (q, k, v))
+    scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(q.shape[-1])
+    out, lse = _FlashAttn.apply(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, scale,
+                                *_window(causal, window_size))
+    return (out, lse) if return_softmax_lse else out
+
+
+def flash_attn_with_kvcache(
+    q: Tensor, k_cache: Tensor, v_cache: Tensor, k: Tensor | None = None, v: Tensor | None = None, *,
+    cache_seqlens: Tensor, causal: bool = False, window_size: tuple[int, int] = (-1, -1),
+    softmax_scale: float | None = None, return_softmax_lse: bool = False,
+):
+    """Writes k/v (batch, new, kv_heads, head_dim) into the caches (batch, capacity,
+    kv_heads, head_dim) at cache_seqlens[b] onward, then attends q over each sequence's
+    cache_seqlens[b] + new keys. The caller advances cache_seqlens. Forward only.
+    Writes that would land at or beyond the capacity are dropped."""
+    _check(q, k_cache, v_cache)
+    if k_cache.stride(-1) != 1 or v_cache.stride(-1) != 1:
+        raise ValueError("the caches need a contiguous last dimension")
+    q = _last_dim_contiguous(q)
+    seqused = cache_seqlens.to(torch.int32)
+    if k is not None and v is not None:
+        if _compiling():
+            _kv_append_op(k_cache, v_cache, k, v, seqused)
+        else:
+            _kv_append(k_cache, v_cache, k, v, seqused)
+        seqused = seqused + k.shape[1]
+    scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(q.shape[-1])
+    out, lse = _fwd(q, k_cache, v_cache, None, None, seqused, q.shape[1], k_cache.shape[1], scale,
+                    *_window(causal, window_size))
+    return (out, lse) if return_softmax_lse else out

@@ -1,0 +1,45 @@
+"""Shared helpers for the parity tests."""
+
+from __future__ import annotations
+
+import torch
+
+
+def assert_close(actual, expected):
+    """The reference's tolerance (tests/test_flash_attn.py:37-40): relative to the largest
+    reference value, bf16 inputs/outputs."""
+    tol = 2e-2 * expected.abs().max().item() + 1e-3
+    torch.testing.assert_close(actual.float().cpu(), expected.float().cpu(), rtol=0, atol=tol)
+
+
+def north_star_errors(actual, expected):
+    """(max-abs, mean-abs) error against an fp32 reference."""
+    d = (actual.float() - expected.float().to(actual.device)).abs()
+    return d.max().item(), d.mean().item()
+
+
+def assert_north_star(actual, expected, max_abs=2e-2, mean_abs=2e-3, what=""):
+    """Absolute bounds: max-abs 2e-2 and mean-abs 2e-3 against the fp32 reference."""
+    mx, mn = north_star_errors(actual, expected)
+    assert mx <= max_abs and mn <= mean_abs, f"{what}: max-abs {mx:.3e} (<= {max_abs}), mean-abs {mn:.3e} (<= {mean_abs})"
+
+
+def assert_lse(actual, expected, tol=1e-3, what="lse"):
+    a, e = actual.float().cpu(), expected.float().cpu()
+    inf_a, inf_e = torch.isinf(a), torch.isinf(e)
+    assert torch.equal(inf_a, inf_e), f"{what}: +inf rows differ"
+    d = (a[~inf_a] - e[~inf_e]).abs()
+    mx = d.max().item() if d.numel() else 0.0
+    assert mx <= tol, f"{what}: max-abs {mx:.3e} > {tol}"
+
+
+def random_qkv(batch, seqlen_q, seqlen_k, heads, kv_heads, head_dim, packed=False, dtype=torch.bfloat16,
+               device="cuda", requires_grad=True):
+    """tests/test_flash_attn.py:31-34, drawn on the CPU from the global seed so the GPU box
+    and any torch build agree, then moved."""
+    lead_q, lead_k = ((seqlen_q,), (seqlen_k,)) if packed else ((batch, seqlen_q), (batch, seqlen_k))
+
+    def make(*shape):
+        return torch.randn(*shape).to(dtype).to(device).requires_grad_(requires_grad)
+
+    return make(*lead_q, heads, head_dim), make(*lead_k, kv_heads, head_dim), make(*lead_k, kv_heads, head_dim)
