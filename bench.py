@@ -1,0 +1,334 @@
+"""Benchmark of the MI355X FlashAttention path (one GPU).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg2] [--quick]
+
+One "step" is one pass of the hot path over one batch of synthetic input. The headline
+workload is BASELINE config 2 (GQA varlen causal, 8 packed documents, 8248 tokens, Hq=16,
+Hkv=4, D=64, bf16), run as forward + backward through the public API (the north-star
+target is fwd+bwd on this 8K-token GQA varlen shape). The step is captured once in a HIP
+graph and replayed, so host-side launch overhead does not pollute a ~100 us workload.
+FLOPs follow the reference's convention (scripts/benchmark_attention.py:49-50, 86):
+F_fwd = 4 * visible pairs * Hq * D, F_fwd+bwd = 3.5 * F_fwd.
+
+Printed: ONE JSON line with the headline value, a "roofline" object for the step's
+dominant kernel (its algorithmic FLOPs / its average duration measured with HIP events on
+its launch stream), a "cpu_baseline" object (the oracle's fp32 CPU attention on a bounded
+sample, timed on this host's cores), and a "configs" object with every other BASELINE
+config (fwd / fwd+bwd TFLOP/s, decode GB/s, fractions of peak).
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+from myk_llm_amd import _lib, flash_attn_func, flash_attn_varlen_func, flash_attn_with_kvcache  # noqa: E402
+from myk_llm_amd import flash_attn as fa  # noqa: E402
+from myk_llm_amd.bench_configs import BF16_PEAK_TFLOPS, HBM_PEAK_GBS, make_inputs, workloads  # noqa: E402
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# --- timing helpers -------------------------------------------------------------------------
+
+
+def time_events(fn, reps: int, warmup: int = 2) -> float:
+    """Average ms per call of fn (launches on torch's current stream), HIP events around reps."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def capture(fn, warmup: int = 3):
+    """Capture fn into a HIP graph (warm-up on a side stream first, as torch requires)."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(warmup):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+# --- direct C-ABI launches of single kernels (for per-kernel durations) -------------------------
+
+
+class KernelCalls:
+    """Prepared C-ABI calls of each kernel of the attention step on fixed buffers."""
+
+    def __init__(self, q, k, v, cu, max_q, max_k, scale, wl, wr, dout=None):
+        self.L = _lib.lib()
+        q, k, v = fa._kernel_ready(q), fa._kernel_ready(k), fa._kernel_ready(v)
+        varlen = cu is not None
+        rows = q.shape[0] if varlen else q.shape[0] * q.shape[1]
+        self.out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        self.lse = torch.empty((q.shape[-2], rows), dtype=torch.float32, device=q.device)
+        self.fp = fa._fwd_params(q, k, v, self.out, self.lse, cu, cu, None, max_q, max_k, scale, wl, wr)
+        self.keep = [q, k, v, cu]
+        self.stream = torch.cuda.current_stream().cuda_stream
+        _lib.check(self.L.mykfa_fwd(ctypes.byref(self.fp), self.stream))
+        if dout is not None:
+            dout = fa._kernel_ready(dout)
+            self.dq, self.dk, self.dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+            self.delta = torch.empty_like(self.lse)
+            p = _lib.BwdParams()
+            p.fwd = self.fp
+            p.dout, p.dq, p.dk, p.dv = dout.data_ptr(), self.dq.data_ptr(), self.dk.data_ptr(), self.dv.data_ptr()
+            p.delta = self.delta.data_ptr()
+            p.do_batch_stride, p.do_token_stride, p.do_head_stride = fa._strides(dout)
+            p.dq_batch_stride, p.dq_token_stride, p.dq_head_stride = fa._strides(self.dq)
+            p.dk_batch_stride, p.dk_token_stride, p.dk_head_stride = fa._strides(self.dk)
+            p.dv_batch_stride, p.dv_token_stride, p.dv_head_stride = fa._strides(self.dv)
+            self.bp = p
+            self.keep.append(dout)
+
+    def fwd(self):
+        _lib.check(self.L.mykfa_fwd(ctypes.byref(self.fp), self.stream))
+
+    def preprocess(self):
+        _lib.check(self.L.mykfa_bwd_preprocess(ctypes.byref(self.bp), self.stream))
+
+    def dkdv(self):
+        _lib.check(self.L.mykfa_bwd_dkdv(ctypes.byref(self.bp), self.stream))
+
+    def dq_(self):
+        _lib.check(self.L.mykfa_bwd_dq(ctypes.byref(self.bp), self.stream))
+
+
+# --- workloads ----------------------------------------------------------------------------------
+
+
+def attention_step(w, inp, backward: bool):
+    """The public-API call of workload w (+ autograd backward)."""
+    if w.kind == "varlen":
+        q, k, v = (inp[n].requires_grad_(backward) for n in ("q", "k", "v"))
+        cu, mx = inp["cu_seqlens"], inp["max_seqlen"]
+
+        def fwd():
+            return flash_attn_varlen_func(q, k, v, cu, cu, mx, mx, causal=True, window_size=w.window_size)
+    else:
+        q, k, v = (inp[n].requires_grad_(backward) for n in ("q", "k", "v"))
+
+        def fwd():
+            return flash_attn_func(q, k, v, causal=True, window_size=w.window_size)
+
+    if not backward:
+        return fwd
+    dout = inp["dout"]
+
+    def step():
+        out = fwd()
+        return torch.autograd.grad(out, (q, k, v), dout)
+
+    return step
+
+
+def measure_prefill(w, steps: int, warmup: int, backward: bool, use_graph: bool = True):
+    inp = make_inputs(w, device="cuda", with_grad_out=backward)
+    step = attention_step(w, inp, backward)
+    if use_graph:
+        g = capture(step, warmup)
+        ms = time_events(g.replay, steps, warmup=1)
+    else:
+        ms = time_events(step, steps, warmup)
+    flops = w.fwd_flops * (3.5 if backward else 1.0)
+    # Per-kernel durations on the same inputs, through the C ABI on torch's current stream.
+    scale = 1.0 / (w.head_dim ** 0.5)
+    wl, wr = fa._window(True, w.window_size)
+    cu = inp.get("cu_seqlens")
+    mq = inp["max_seqlen"] if cu is not None else w.seqlen
+    kc = KernelCalls(inp["q"].detach(), inp["k"].detach(), inp["v"].detach(), cu, mq, mq, scale, wl, wr,
+                     inp["dout"] if backward else None)
+    reps = max(steps, 10)
+    kern = {"fwd": time_events(kc.fwd, reps)}
+    if backward:
+        kern["bwd_preprocess"] = time_events(kc.preprocess, reps)
+        kern["bwd_dkdv"] = time_events(kc.dkdv, reps)
+        kern["bwd_dq"] = time_events(kc.dq_, reps)
+    # Algorithmic FLOPs per launch (convention split: fwd = 2 products; of the 5 backward
+    # products, dK/dV's kernel owns S, dP, dV, dK = 2.0 F_fwd and dQ's owns dQ = 0.5 F_fwd).
+    algo = {"fwd": w.fwd_flops, "bwd_dkdv": 2.0 * w.fwd_flops, "bwd_dq": 0.5 * w.fwd_flops, "bwd_preprocess": 0.0}
+    del inp, step, kc
+    return ms, flops, kern, algo
+
+
+def measure_decode(w, steps: int, warmup: int):
+    """flash_attn_with_kvcache (append + split-K decode + merge) captured in a graph; replays
+    rotate over independent cache sets totalling > 2 GB so the 256 MB Infinity Cache cannot
+    hold the working set."""
+    g0 = torch.Generator(device="cuda").manual_seed(0)
+    b = len(w.cache_seqlens)
+    nsets = 2
+    sets = []
+    for _ in range(nsets):
+        kc = torch.randn(b, w.capacity, w.kv_heads, w.head_dim, device="cuda", generator=g0).to(torch.bfloat16)
+        vc = torch.randn(b, w.capacity, w.kv_heads, w.head_dim, device="cuda", generator=g0).to(torch.bfloat16)
+        sets.append((kc, vc))
+    q = torch.randn(b, w.nq, w.heads, w.head_dim, device="cuda", generator=g0).to(torch.bfloat16)
+    kn = torch.randn(b, w.nq, w.kv_heads, w.head_dim, device="cuda", generator=g0).to(torch.bfloat16)
+    vn = torch.randn(b, w.nq, w.kv_heads, w.head_dim, device="cuda", generator=g0).to(torch.bfloat16)
+    lens = torch.tensor(w.cache_seqlens, dtype=torch.int32, device="cuda")
+    graphs = []
+    for kc, vc in sets:
+        def step(kc=kc, vc=vc):
+            return flash_attn_with_kvcache(q, kc, vc, kn, vn, cache_seqlens=lens, causal=True)
+        graphs.append(capture(step, warmup))
+    it = [0]
+
+    def replay():
+        graphs[it[0] % nsets].replay()
+        it[0] += 1
+
+    ms = time_events(replay, steps * nsets, warmup=nsets)
+    del sets, graphs
+    return ms
+
+
+# --- CPU baseline ---------------------------------------------------------------------------------
+
+
+def cpu_baseline(w, budget_s: float = 12.0):
+    """The reference's CPU attention path (fp32 einsum reference(), restated in oracle/) with
+    CPU autograd for the backward, looping per document, on this host's cores; documents are
+    taken in order until budget_s of CPU work has been spent (a bounded sample)."""
+    from oracle.attention import reference
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    inp = make_inputs(w, device="cpu", with_grad_out=True)
+    cu = inp["cu_seqlens"].tolist()
+    done_pairs, t_total, docs = 0, 0.0, 0
+    for i, (a, b) in enumerate(zip(cu, cu[1:])):
+        q, k, v = (inp[n][a:b][None].float().requires_grad_() for n in ("q", "k", "v"))
+        do = inp["dout"][a:b][None].float()
+        t0 = time.perf_counter()
+        out = reference(q, k, v, True, w.window_size)
+        torch.autograd.grad(out, (q, k, v), do)
+        t_total += time.perf_counter() - t0
+        n = b - a
+        done_pairs += n * (n + 1) // 2
+        docs += 1
+        if t_total >= budget_s:
+            break
+    flops = 3.5 * 4.0 * done_pairs * w.heads * w.head_dim
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "")
+    except OSError:
+        pass
+    return {"value": round(flops / t_total / 1e12, 6), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"fwd+bwd fp32 oracle (reference() restated, CPU autograd) over the first {docs} of "
+                      f"{len(cu) - 1} {w.name} documents ({done_pairs} visible pairs), {t_total:.1f} s; {model}",
+            "seconds": round(t_total, 3)}
+
+
+# --- main -------------------------------------------------------------------------------------------
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="cfg2")
+    ap.add_argument("--quick", action="store_true", help="headline only: no other configs, no CPU baseline")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--eager", action="store_true", help="time eager calls instead of graph replays")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for {args.gpus}); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    _lib.lib()
+    W = workloads()
+    w = W[args.workload]
+    log(f"headline {w.name}: fwd+bwd, steps={args.steps} warmup={args.warmup}")
+    torch.cuda.synchronize()
+    ms, flops, kern, algo = measure_prefill(w, args.steps, args.warmup, backward=True, use_graph=not args.eager)
+    value = flops / (ms * 1e-3) / 1e12
+    dom = max((k for k in kern if algo.get(k, 0) > 0), key=lambda k: kern[k])
+    achieved = algo[dom] / (kern[dom] * 1e-3) / 1e12
+    log(f"  {ms:.4f} ms/step, {value:.1f} TFLOP/s; kernels (ms): " + ", ".join(f"{k}={v:.4f}" for k, v in kern.items()))
+    configs = {}
+    if not args.quick:
+        for name in ("cfg2", "cfg3", "cfg4"):
+            wk = W[name]
+            for bwd in ((False, True) if name != "cfg2" else (False,)):
+                log(f"config {wk.name} {'fwd+bwd' if bwd else 'fwd'}")
+                m, f, kk, _ = measure_prefill(wk, max(10, args.steps // 2), 3, backward=bwd)
+                t = f / (m * 1e-3) / 1e12
+                configs[f"{name}_{'fwdbwd' if bwd else 'fwd'}"] = {
+                    "workload": wk.name, "ms": round(m, 5), "TFLOP/s": round(t, 2),
+                    "frac_of_bf16_peak": round(t / BF16_PEAK_TFLOPS, 4),
+                    "kernel_ms": {k: round(v, 5) for k, v in kk.items()}}
+                log(f"  {m:.4f} ms, {t:.1f} TFLOP/s")
+        for name in ("cfg5", "cfg5_mtp"):
+            wk = W[name]
+            log(f"config {wk.name} decode")
+            m = measure_decode(wk, max(10, args.steps // 2), 3)
+            gbs = wk.decode_bytes / (m * 1e-3) / 1e9
+            configs[name] = {"workload": wk.name, "ms": round(m, 5), "GB/s": round(gbs, 1),
+                             "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "bytes": int(wk.decode_bytes)}
+            log(f"  {m * 1e3:.1f} us, {gbs:.0f} GB/s")
+    cpu = None
+    if not (args.quick or args.no_cpu):
+        log("cpu baseline")
+        cpu = cpu_baseline(w)
+        log(f"  {cpu}")
+    line = {
+        "metric": "attn fwd/fwd+bwd TFLOP/s + decode GB/s, % of MI355X peak, 1 GPU",
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q/k/v/dO, BASELINE config recipes)",
+        "config": {"workload": w.name, "pass": "fwd+bwd", "tokens": sum(w.lengths), "docs": len(w.lengths),
+                   "heads": w.heads, "kv_heads": w.kv_heads, "head_dim": w.head_dim,
+                   "timing": "eager" if args.eager else "hipgraph replay", "parallelism": "none (1 GPU)"},
+        "frac_of_bf16_peak": round(value / BF16_PEAK_TFLOPS, 4),
+        "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2), "peak": BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "kernel_ms": round(kern[dom], 5)},
+        "kernels_ms": {k: round(v, 5) for k, v in kern.items()},
+        "cpu_baseline": cpu,
+        "configs": configs,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

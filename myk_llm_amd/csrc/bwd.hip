@@ -18,9 +18,6 @@ namespace mykfa {
 
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
-
 struct BwdArgs {
     const uint16_t* q;
     const uint16_t* k;
@@ -74,36 +71,6 @@ __global__ __launch_bounds__(256) void bwd_preprocess_kernel(BwdArgs a) {
 
 // ---- 2. dK / dV -------------------------------------------------------------------------
 
-template <int D>
-struct RowTileLoader {  // BM x D tile of a (token, head) tensor, rows beyond len are zero
-    static constexpr int CPR = D / 8;
-    static constexpr int BM = 32;
-    static constexpr int CHUNKS = BM * CPR;
-    static constexpr int PER = (CHUNKS + kThreads - 1) / kThreads;
-    s16x8 r[PER];
-    __device__ inline void load(const uint16_t* base, int64_t tstride, int m0, int len, int tid) {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int idx = tid + i * kThreads;
-            const int row = idx / CPR, ch = idx % CPR;
-            s16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
-            if ((CHUNKS % kThreads == 0 || idx < CHUNKS) && m0 + row < len)
-                v = ld16(base + (int64_t)(m0 + row) * tstride + ch * 8);
-            r[i] = v;
-        }
-    }
-    __device__ inline void store(uint16_t* lds, int tid) const {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int idx = tid + i * kThreads;
-            if (CHUNKS % kThreads == 0 || idx < CHUNKS) {
-                const int row = idx / CPR, ch = idx % CPR;
-                *reinterpret_cast<s16x8*>(lds + row * D + ((ch ^ lds_swz<D>(row)) << 3)) = r[i];
-            }
-        }
-    }
-};
-
 // A operand (32 rows x 16 k) of a row-major LDS tile at rows perm32(l32), k-step kk.
 template <int D>
 __device__ inline s16x8 lds_row_op(const uint16_t* tile, int rbase, int l32, int g, int kk) {
@@ -125,20 +92,32 @@ __device__ inline s16x8 lds_tr_op(const uint16_t* tile, int db, int kb, int lane
     return v;
 }
 
-template <int D, typename T>
-__global__ __launch_bounds__(kThreads) void bwd_dkdv_kernel(BwdArgs a) {
+// One workgroup = NW waves over one KV head: hpw = gcd(group, NW) waves share each 32-key
+// block, each streaming a different query head of the group (heads hs, hs + hpw, ...), so a
+// key block's serial chain is group / hpw heads long instead of group. Each wave keeps its
+// keys' K and V in registers as B operands and streams its own (Q, dO, lse, delta) query
+// tiles through a wave-private asynchronous LDS ring: the main loop has no workgroup
+// barrier. The hpw partial dK/dV of a key block are summed through LDS in a fixed order
+// (deterministic) at the end.
+template <int D, int NW, int STAGES, typename T>
+__global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
     constexpr int KD = D / 16;
     constexpr int DB = (D + 31) / 32;
-    constexpr int BMQ = 32;           // queries per step
-    constexpr int BNK = 32 * kWaves;  // keys per workgroup
-    __shared__ __attribute__((aligned(16))) uint16_t sq[2][BMQ * D];
-    __shared__ __attribute__((aligned(16))) uint16_t sdo[2][BMQ * D];
-    __shared__ __attribute__((aligned(16))) float slse[2][BMQ];
-    __shared__ __attribute__((aligned(16))) float sdel[2][BMQ];
+    constexpr int BMQ = 32;
+    constexpr int CPR = D / 8;
+    constexpr int QLOADS = BMQ * CPR / 64;          // 64-lane loads per 32 x D tile
+    constexpr int LOADS = 2 * QLOADS + 2;           // Q, dO, lse, delta
+    constexpr int TILE = BMQ * D;                   // elements of one 32 x D tile
+    constexpr int STAGE = 2 * TILE + 2 * BMQ * 2;   // Q, dO and 64 floats, in 16-bit units
+    static_assert(QLOADS >= 1, "tile must be whole 64-lane loads");
+    static_assert(NW * STAGES * STAGE >= NW * DB * 16 * 64 * 2, "reduction buffer fits the ring");
+    __shared__ __attribute__((aligned(16))) uint16_t smem[NW][STAGES][STAGE];
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int l32 = lane & 31, g = lane >> 5;
-    const int n0 = blockIdx.x * BNK;  // causal: the first key blocks see the most queries
+    const int hpw = a.hpw, kpw = NW / hpw;
+    const int kb_w = wave / hpw, hs = wave % hpw;
+    const int n0 = blockIdx.x * 32 * kpw;  // causal: the first key blocks see the most queries
     const int b = blockIdx.y, kvh = blockIdx.z;
     SeqInfo ks = seq_info(b, a.cu_k, nullptr, a.seqlen_k, false);
     const int k_len = ks.len;
@@ -150,12 +129,12 @@ __global__ __launch_bounds__(kThreads) void bwd_dkdv_kernel(BwdArgs a) {
     const int lo_t = band_lo(q_len, k_len, a.wr), hi_t = band_hi(q_len, k_len, a.wl);
     const int lo_f = band_lo(k_len, q_len, a.wl), hi_f = band_hi(k_len, q_len, a.wr);
 
-    const int wg_bs = k_len - n0 < BNK ? k_len - n0 : BNK;
-    const Ranges wgr = block_ranges(n0, wg_bs, lo_t, hi_t, q_len, BMQ);
-    const int nw0 = n0 + 32 * wave;
+    const int nw0 = n0 + 32 * kb_w;
     const int bs = k_len - nw0 < 32 ? k_len - nw0 : 32;
     Ranges wr = {0, 0, 0, 0};
     if (bs > 0) wr = block_ranges(nw0, bs, lo_t, hi_t, q_len, BMQ);
+    const int ntiles = (bs > 0 && wr.hi > wr.lo) ? (wr.hi - wr.lo + BMQ - 1) / BMQ : 0;
+    const int iters = ntiles * (a.group / hpw);
 
     // K, V rows of this wave as B operands: lane holds K[nw0 + l32][16 kk + 8 g + i].
     s16x8 kop[KD], vop[KD];
@@ -170,105 +149,137 @@ __global__ __launch_bounds__(kThreads) void bwd_dkdv_kernel(BwdArgs a) {
             vop[kk] = key < k_len ? ld16(vp + 16 * kk + 8 * g) : z;
         }
     }
+    wait_vmcnt<0>();  // K/V landed before the ring's loads share the counter
     f32x16 dk[DB], dv[DB];
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
         for (int r = 0; r < 16; ++r) dk[db][r] = dv[db][r] = 0.f;
 
-    const int ntiles = wgr.hi > wgr.lo ? (wgr.hi - wgr.lo + BMQ - 1) / BMQ : 0;
-    const int iters = ntiles * a.group;
-    RowTileLoader<D> ql, dol;
-    float lse_r = 0.f, del_r = 0.f;
+    uint16_t* ring = smem[wave][0];
     auto issue = [&](int it) {
-        const int hg = it / ntiles, m0 = wgr.lo + (it % ntiles) * BMQ;
-        const int h = kvh * a.group + hg;
-        ql.load(a.q + (int64_t)b * a.qbs + qs.tok0 * a.qts + (int64_t)h * a.qhs, a.qts, m0, q_len, tid);
-        dol.load(a.dout + (int64_t)b * a.dobs + qs.tok0 * a.dots + (int64_t)h * a.dohs, a.dots, m0, q_len, tid);
-        if (tid < 2 * BMQ) {
-            const int r = tid & (BMQ - 1);
-            const bool ok = m0 + r < q_len;
-            const int64_t off = (int64_t)h * a.lse_hs + qs.row0 + m0 + r;
-            if (tid < BMQ) lse_r = ok ? a.lse[off] : INFINITY;
-            else del_r = ok ? a.delta[off] : 0.f;
+        const int h = kvh * a.group + hs + hpw * (it / ntiles);
+        const int m0 = wr.lo + (it % ntiles) * BMQ;
+        uint16_t* st = ring + (it % STAGES) * STAGE;
+        const uint16_t* qb = a.q + (int64_t)b * a.qbs + qs.tok0 * a.qts + (int64_t)h * a.qhs;
+        const uint16_t* db_ = a.dout + (int64_t)b * a.dobs + qs.tok0 * a.dots + (int64_t)h * a.dohs;
+        const i32x4 rq = rows_rsrc(qb, q_len, a.qts, D);
+        const i32x4 rd = rows_rsrc(db_, q_len, a.dots, D);
+#pragma unroll
+        for (int j = 0; j < QLOADS; ++j) {
+            const int p = j * 64 + lane;
+            const int row = p / CPR, phys = p % CPR;
+            const int logical = phys ^ lds_swz<D>(row);
+            const unsigned oq = (unsigned)((m0 + row) * (int)(a.qts * 2) + logical * 16);
+            const unsigned od = (unsigned)((m0 + row) * (int)(a.dots * 2) + logical * 16);
+            dma16(rq, lds_addr(st + j * 512), oq);
+            dma16(rd, lds_addr(st + TILE + j * 512), od);
         }
+        // lse into floats [0, 32), delta into [32, 64) of the stage's float area; rows at or
+        // beyond q_len read 0 (their probabilities are masked to 0).
+        const float* lb = a.lse + (int64_t)h * a.lse_hs + qs.row0;
+        const float* dl = a.delta + (int64_t)h * a.lse_hs + qs.row0;
+        const int64_t fbytes = (int64_t)q_len * 4;
+        const i32x4 rl = buffer_rsrc(lb, fbytes), rdl = buffer_rsrc(dl, fbytes);
+        const uint32_t fl = lds_addr(st + 2 * TILE);
+        if (lane < 32) dma4(rl, fl, (unsigned)((m0 + lane) * 4));
+        if (lane >= 32) dma4(rdl, fl, (unsigned)((m0 + lane - 32) * 4));
     };
-    auto commit = [&](int buf) {
-        ql.store(sq[buf], tid);
-        dol.store(sdo[buf], tid);
-        if (tid < BMQ) slse[buf][tid] = lse_r;
-        else if (tid < 2 * BMQ) sdel[buf][tid - BMQ] = del_r;
-    };
-    if (iters > 0) {
-        issue(0);
-        commit(0);
-    }
-    int buf = 0;
+#pragma unroll
+    for (int t = 0; t < STAGES - 1; ++t)
+        if (t < iters) issue(t);
+
     for (int it = 0; it < iters; ++it) {
-        __syncthreads();
-        const bool more = it + 1 < iters;
-        if (more) issue(it + 1);
-        const int m0 = wgr.lo + (it % ntiles) * BMQ;
-        const bool active = bs > 0 && m0 < wr.hi && m0 + BMQ > wr.lo;
-        if (active) {
-            const bool masked = !(m0 >= wr.mid_lo && m0 + BMQ <= wr.mid_hi);
-            const uint16_t* Qs = sq[buf];
-            const uint16_t* DOs = sdo[buf];
-            // S = Q K^T and dP = dO V^T: lane column = key nw0 + l32, registers = queries.
-            f32x16 s, dp;
+        const int after = iters - 1 - it < STAGES - 2 ? iters - 1 - it : STAGES - 2;
+        ring_wait<LOADS, STAGES>(after);
+        wait_lgkmcnt0();  // this wave's reads of the stage about to be refilled have returned
+        if (it + STAGES - 1 < iters) issue(it + STAGES - 1);
+        const int m0 = wr.lo + (it % ntiles) * BMQ;
+        const bool masked = !(m0 >= wr.mid_lo && m0 + BMQ <= wr.mid_hi);
+        const uint16_t* st = ring + (it % STAGES) * STAGE;
+        const uint16_t* Qs = st;
+        const uint16_t* DOs = st + TILE;
+        const float* fl = reinterpret_cast<const float*>(st + 2 * TILE);
+        // S = Q K^T and dP = dO V^T: lane column = key nw0 + l32, registers = queries.
+        f32x16 s, dp;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
+        for (int r = 0; r < 16; ++r) s[r] = dp[r] = 0.f;
 #pragma unroll
-            for (int kk = 0; kk < KD; ++kk) {
-                s = T::mfma32(lds_row_op<D>(Qs, 0, l32, g, kk), kop[kk], s);
-                dp = T::mfma32(lds_row_op<D>(DOs, 0, l32, g, kk), vop[kk], dp);
+        for (int kk = 0; kk < KD; ++kk) {
+            s = T::mfma32(lds_row_op<D>(Qs, 0, l32, g, kk), kop[kk], s);
+            dp = T::mfma32(lds_row_op<D>(DOs, 0, l32, g, kk), vop[kk], dp);
+        }
+        const int key = nw0 + l32;
+        s16x8 pb[2], dsb[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            // Rows 16 kb + 8 g + i, i = 0..7 (registers 8 kb + i).
+            const f32x4 l0 = *reinterpret_cast<const f32x4*>(fl + 16 * kb + 8 * g);
+            const f32x4 l1 = *reinterpret_cast<const f32x4*>(fl + 16 * kb + 8 * g + 4);
+            const f32x4 d0 = *reinterpret_cast<const f32x4*>(fl + 32 + 16 * kb + 8 * g);
+            const f32x4 d1 = *reinterpret_cast<const f32x4*>(fl + 32 + 16 * kb + 8 * g + 4);
+            float pv[8], dsv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float lse_i = i < 4 ? l0[i] : l1[i - 4];
+                const float del_i = i < 4 ? d0[i] : d1[i - 4];
+                float p = fast_exp2(s[8 * kb + i] * a.qk_scale - lse_i);
+                if (masked) {
+                    const int qi = m0 + 16 * kb + 8 * g + i;
+                    const int rel = key - qi;
+                    p = (rel >= lo_f && rel <= hi_f && qi < q_len && key < k_len) ? p : 0.f;
+                }
+                pv[i] = p;
+                dsv[i] = p * (dp[8 * kb + i] - del_i);
             }
-            const int key = nw0 + l32;
-            s16x8 pb[2], dsb[2];
+            u32x4 pw = {T::pack2(pv[0], pv[1]), T::pack2(pv[2], pv[3]), T::pack2(pv[4], pv[5]),
+                        T::pack2(pv[6], pv[7])};
+            u32x4 dw = {T::pack2(dsv[0], dsv[1]), T::pack2(dsv[2], dsv[3]), T::pack2(dsv[4], dsv[5]),
+                        T::pack2(dsv[6], dsv[7])};
+            pb[kb] = __builtin_bit_cast(s16x8, pw);
+            dsb[kb] = __builtin_bit_cast(s16x8, dw);
+        }
+        // dV^T += dO^T P, dK^T += Q^T dS.
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
-                // Rows 16 kb + 8 g + i, i = 0..7 (registers 8 kb + i).
-                const f32x4 l0 = *reinterpret_cast<const f32x4*>(&slse[buf][16 * kb + 8 * g]);
-                const f32x4 l1 = *reinterpret_cast<const f32x4*>(&slse[buf][16 * kb + 8 * g + 4]);
-                const f32x4 d0 = *reinterpret_cast<const f32x4*>(&sdel[buf][16 * kb + 8 * g]);
-                const f32x4 d1 = *reinterpret_cast<const f32x4*>(&sdel[buf][16 * kb + 8 * g + 4]);
-                float pv[8], dsv[8];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const float lse_i = i < 4 ? l0[i] : l1[i - 4];
-                    const float del_i = i < 4 ? d0[i] : d1[i - 4];
-                    float p = fast_exp2(s[8 * kb + i] * a.qk_scale - lse_i);
-                    if (masked) {
-                        const int qi = m0 + 16 * kb + 8 * g + i;
-                        const int rel = key - qi;
-                        p = (rel >= lo_f && rel <= hi_f && qi < q_len && key < k_len) ? p : 0.f;
-                    }
-                    pv[i] = p;
-                    dsv[i] = p * (dp[8 * kb + i] - del_i);
-                }
-                u32x4 pw = {T::pack2(pv[0], pv[1]), T::pack2(pv[2], pv[3]), T::pack2(pv[4], pv[5]),
-                            T::pack2(pv[6], pv[7])};
-                u32x4 dw = {T::pack2(dsv[0], dsv[1]), T::pack2(dsv[2], dsv[3]), T::pack2(dsv[4], dsv[5]),
-                            T::pack2(dsv[6], dsv[7])};
-                pb[kb] = __builtin_bit_cast(s16x8, pw);
-                dsb[kb] = __builtin_bit_cast(s16x8, dw);
+                dv[db] = T::mfma32(lds_tr_op<D>(DOs, db, kb, lane), pb[kb], dv[db]);
+                dk[db] = T::mfma32(lds_tr_op<D>(Qs, db, kb, lane), dsb[kb], dk[db]);
             }
-            // dV^T += dO^T P, dK^T += Q^T dS.
+    }
+
+    // Sum the hpw partials of each key block in a fixed order (waves hs = 1.. into hs = 0).
+    if (hpw > 1) {
+        float* red = reinterpret_cast<float*>(&smem[0][0][0]);
+        constexpr int PART = DB * 16 * 64;  // floats of one wave's accumulator set
 #pragma unroll
-            for (int db = 0; db < DB; ++db)
+        for (int pass = 0; pass < 2; ++pass) {
+            f32x16* accs = pass == 0 ? dk : dv;
+            __syncthreads();
+            if (hs != 0) {
+                float* dst = red + wave * PART;
 #pragma unroll
-                for (int kb = 0; kb < 2; ++kb) {
-                    dv[db] = T::mfma32(lds_tr_op<D>(DOs, db, kb, lane), pb[kb], dv[db]);
-                    dk[db] = T::mfma32(lds_tr_op<D>(Qs, db, kb, lane), dsb[kb], dk[db]);
+                for (int db = 0; db < DB; ++db)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) dst[(db * 16 + r) * 64 + lane] = accs[db][r];
+            }
+            __syncthreads();
+            if (hs == 0) {
+                for (int o = 1; o < hpw; ++o) {
+                    const float* src = red + (wave + o) * PART;
+#pragma unroll
+                    for (int db = 0; db < DB; ++db)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) accs[db][r] += src[(db * 16 + r) * 64 + lane];
                 }
+            }
         }
-        if (more) commit(buf ^ 1);
-        buf ^= 1;
     }
 
     // Store dK * sm_scale and dV (flash_attn.py:312-314); lane column = key, rows = d.
     const int key = nw0 + l32;
-    if (bs > 0 && key < k_len) {
+    if (hs == 0 && bs > 0 && key < k_len) {
         uint16_t* dkp = a.dk + (int64_t)b * a.dkbs + (ks.tok0 + key) * a.dkts + (int64_t)kvh * a.dkhs;
         uint16_t* dvp = a.dv + (int64_t)b * a.dvbs + (ks.tok0 + key) * a.dvts + (int64_t)kvh * a.dvhs;
 #pragma unroll
@@ -290,46 +301,18 @@ __global__ __launch_bounds__(kThreads) void bwd_dkdv_kernel(BwdArgs a) {
 
 // ---- 3. dQ ------------------------------------------------------------------------------
 
-template <int D, int BN>
-struct KeyTileLoader {
-    static constexpr int CPR = D / 8;
-    static constexpr int CHUNKS = BN * CPR;
-    static constexpr int PER = (CHUNKS + kThreads - 1) / kThreads;
-    s16x8 r[PER];
-    __device__ inline void load(const uint16_t* base, int64_t tstride, int n0, int len, int tid) {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int idx = tid + i * kThreads;
-            const int row = idx / CPR, ch = idx % CPR;
-            s16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
-            if ((CHUNKS % kThreads == 0 || idx < CHUNKS) && n0 + row < len)
-                v = ld16(base + (int64_t)(n0 + row) * tstride + ch * 8);
-            r[i] = v;
-        }
-    }
-    __device__ inline void store(uint16_t* lds, int tid) const {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int idx = tid + i * kThreads;
-            if (CHUNKS % kThreads == 0 || idx < CHUNKS) {
-                const int row = idx / CPR, ch = idx % CPR;
-                *reinterpret_cast<s16x8*>(lds + row * D + ((ch ^ lds_swz<D>(row)) << 3)) = r[i];
-            }
-        }
-    }
-};
-
-template <int D, int BN, typename T>
-__global__ __launch_bounds__(kThreads) void bwd_dq_kernel(BwdArgs a) {
+template <int D, int BN, int NW, int STAGES, typename T>
+__global__ __launch_bounds__(NW * 64) void bwd_dq_kernel(BwdArgs a) {
     constexpr int KD = D / 16;
     constexpr int DB = (D + 31) / 32;
     constexpr int NB = BN / 32;
     constexpr int KB = BN / 16;
-    __shared__ __attribute__((aligned(16))) uint16_t smem[2][2][BN * D];
+    using Ring = TileRing<D, BN, 2, NW>;
+    __shared__ __attribute__((aligned(16))) uint16_t smem[STAGES][2][BN * D];
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int l32 = lane & 31, g = lane >> 5;
-    const int tpw = kWaves / a.hpw;
+    const int tpw = NW / a.hpw;
     const int mblk = gridDim.x - 1 - blockIdx.x;
     const int b = blockIdx.y;
     const int h_first = blockIdx.z * a.hpw;
@@ -360,6 +343,8 @@ __global__ __launch_bounds__(kThreads) void bwd_dq_kernel(BwdArgs a) {
 
     const uint16_t* kbase = a.k + (int64_t)b * a.kbs + ks.tok0 * a.kts + (int64_t)kvh * a.khs;
     const uint16_t* vbase = a.v + (int64_t)b * a.vbs + ks.tok0 * a.vts + (int64_t)kvh * a.vhs;
+    const i32x4 rsrc[2] = {rows_rsrc(kbase, k_len, a.kts, D), rows_rsrc(vbase, k_len, a.vts, D)};
+    const int tstride[2] = {(int)(a.kts * 2), (int)(a.vts * 2)};
 
     const int qi = s0 + l32;
     const bool q_ok = bs > 0 && qi < q_len;
@@ -381,6 +366,7 @@ __global__ __launch_bounds__(kThreads) void bwd_dq_kernel(BwdArgs a) {
         lse_q = a.lse[off];
         del_q = a.delta[off];
     }
+    wait_vmcnt<0>();  // Q, dO, lse, delta landed before the ring's loads share the counter
 
     f32x16 acc[DB];
 #pragma unroll
@@ -388,67 +374,61 @@ __global__ __launch_bounds__(kThreads) void bwd_dq_kernel(BwdArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
 
-    KeyTileLoader<D, BN> kl, vl;
-    if (wg_hi > wg_lo) {
-        kl.load(kbase, a.kts, wg_lo, k_len, tid);
-        vl.load(vbase, a.vts, wg_lo, k_len, tid);
-        kl.store(smem[0][0], tid);
-        vl.store(smem[0][1], tid);
-    }
-    int buf = 0;
-    for (int n0 = wg_lo; n0 < wg_hi; n0 += BN) {
-        __syncthreads();
-        const bool more = n0 + BN < wg_hi;
-        if (more) {
-            kl.load(kbase, a.kts, n0 + BN, k_len, tid);
-            vl.load(vbase, a.vts, n0 + BN, k_len, tid);
-        }
+    const int ntiles = wg_hi > wg_lo ? (wg_hi - wg_lo + BN - 1) / BN : 0;
+    auto issue = [&](int t) {
+        uint16_t* tiles[2] = {smem[t % STAGES][0], smem[t % STAGES][1]};
+        Ring::issue(rsrc, tstride, tiles, wg_lo + t * BN, wave, lane);
+    };
+#pragma unroll
+    for (int t = 0; t < STAGES - 1; ++t)
+        if (t < ntiles) issue(t);
+
+    for (int t = 0; t < ntiles; ++t) {
+        const int n0 = wg_lo + t * BN;
+        const int after = ntiles - 1 - t < STAGES - 2 ? ntiles - 1 - t : STAGES - 2;
+        ring_wait<Ring::LOADS, STAGES>(after);
+        barrier_lds();
+        if (t + STAGES - 1 < ntiles) issue(t + STAGES - 1);
         const bool active = bs > 0 && n0 < wr.hi && n0 + BN > wr.lo;
-        if (active) {
-            const bool masked = !(n0 >= wr.mid_lo && n0 + BN <= wr.mid_hi);
-            const uint16_t* Ks = smem[buf][0];
-            const uint16_t* Vs = smem[buf][1];
-            s16x8 dsb[KB];
+        if (!active) continue;
+        const bool masked = !(n0 >= wr.mid_lo && n0 + BN <= wr.mid_hi);
+        const uint16_t* Ks = smem[t % STAGES][0];
+        const uint16_t* Vs = smem[t % STAGES][1];
+        s16x8 dsb[KB];
 #pragma unroll
-            for (int nb = 0; nb < NB; ++nb) {
-                f32x16 st, dpt;
+        for (int nb = 0; nb < NB; ++nb) {
+            f32x16 st, dpt;
 #pragma unroll
-                for (int r = 0; r < 16; ++r) st[r] = dpt[r] = 0.f;
+            for (int r = 0; r < 16; ++r) st[r] = dpt[r] = 0.f;
 #pragma unroll
-                for (int kk = 0; kk < KD; ++kk) {
-                    st = T::mfma32(lds_row_op<D>(Ks, nb * 32, l32, g, kk), qop[kk], st);
-                    dpt = T::mfma32(lds_row_op<D>(Vs, nb * 32, l32, g, kk), doop[kk], dpt);
-                }
-                float dsv[16];
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    float p = fast_exp2(st[r] * a.qk_scale - lse_q);
-                    if (masked) {
-                        const int key = n0 + nb * 32 + out_row32(r, g);
-                        const int rel = key - qi;
-                        p = (rel >= lo_off && rel <= hi_off && key < k_len) ? p : 0.f;
-                    }
-                    dsv[r] = p * (dpt[r] - del_q);
-                }
-#pragma unroll
-                for (int half = 0; half < 2; ++half) {
-                    u32x4 w = {T::pack2(dsv[8 * half], dsv[8 * half + 1]), T::pack2(dsv[8 * half + 2], dsv[8 * half + 3]),
-                               T::pack2(dsv[8 * half + 4], dsv[8 * half + 5]),
-                               T::pack2(dsv[8 * half + 6], dsv[8 * half + 7])};
-                    dsb[nb * 2 + half] = __builtin_bit_cast(s16x8, w);
-                }
+            for (int kk = 0; kk < KD; ++kk) {
+                st = T::mfma32(lds_row_op<D>(Ks, nb * 32, l32, g, kk), qop[kk], st);
+                dpt = T::mfma32(lds_row_op<D>(Vs, nb * 32, l32, g, kk), doop[kk], dpt);
             }
-            // dQ^T += K^T dS^T: A operand K[16 kb + 8 g + i][32 db + l32] by transpose read.
+            float dsv[16];
 #pragma unroll
-            for (int db = 0; db < DB; ++db)
+            for (int r = 0; r < 16; ++r) {
+                float p = fast_exp2(st[r] * a.qk_scale - lse_q);
+                if (masked) {
+                    const int key = n0 + nb * 32 + out_row32(r, g);
+                    const int rel = key - qi;
+                    p = (rel >= lo_off && rel <= hi_off && key < k_len) ? p : 0.f;
+                }
+                dsv[r] = p * (dpt[r] - del_q);
+            }
 #pragma unroll
-                for (int kb = 0; kb < KB; ++kb) acc[db] = T::mfma32(lds_tr_op<D>(Ks, db, kb, lane), dsb[kb], acc[db]);
+            for (int half = 0; half < 2; ++half) {
+                u32x4 w = {T::pack2(dsv[8 * half], dsv[8 * half + 1]), T::pack2(dsv[8 * half + 2], dsv[8 * half + 3]),
+                           T::pack2(dsv[8 * half + 4], dsv[8 * half + 5]),
+                           T::pack2(dsv[8 * half + 6], dsv[8 * half + 7])};
+                dsb[nb * 2 + half] = __builtin_bit_cast(s16x8, w);
+            }
         }
-        if (more) {
-            kl.store(smem[buf ^ 1][0], tid);
-            vl.store(smem[buf ^ 1][1], tid);
-        }
-        buf ^= 1;
+        // dQ^T += K^T dS^T: A operand K[16 kb + 8 g + i][32 db + l32] by transpose read.
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) acc[db] = T::mfma32(lds_tr_op<D>(Ks, db, kb, lane), dsb[kb], acc[db]);
     }
 
     if (q_ok) {
@@ -507,7 +487,7 @@ BwdArgs make_args(const mykfa_bwd_params& p) {
     a.qk_scale = f.softmax_scale * 1.4426950408889634f;
     a.sm_scale = f.softmax_scale;
     a.group = f.num_heads / f.num_kv_heads;
-    a.hpw = gcd_int(a.group, kWaves);
+    a.hpw = 1;  // set per kernel shape by its launcher
     a.num_heads = f.num_heads;
     a.batch = f.batch;
     return a;
@@ -529,33 +509,46 @@ hipError_t preprocess_dtype(const BwdArgs& a, int D, hipStream_t s) {
     return hipGetLastError();
 }
 
+template <int D, int NW, int STAGES, typename T>
+hipError_t dkdv_launch(BwdArgs a, int num_kv_heads, hipStream_t s) {
+    a.hpw = gcd_int(a.group, NW);
+    const int keys_per_wg = 32 * (NW / a.hpw);
+    dim3 grid((a.seqlen_k + keys_per_wg - 1) / keys_per_wg, a.batch, num_kv_heads);
+    hipLaunchKernelGGL((bwd_dkdv_kernel<D, NW, STAGES, T>), grid, dim3(NW * 64), 0, s, a);
+    return hipGetLastError();
+}
+
 template <typename T>
 hipError_t dkdv_dtype(const BwdArgs& a, int D, int num_kv_heads, hipStream_t s) {
-    dim3 grid((a.seqlen_k + 32 * kWaves - 1) / (32 * kWaves), a.batch, num_kv_heads);
     switch (D) {
-        case 16: hipLaunchKernelGGL((bwd_dkdv_kernel<16, T>), grid, dim3(kThreads), 0, s, a); break;
-        case 32: hipLaunchKernelGGL((bwd_dkdv_kernel<32, T>), grid, dim3(kThreads), 0, s, a); break;
-        case 64: hipLaunchKernelGGL((bwd_dkdv_kernel<64, T>), grid, dim3(kThreads), 0, s, a); break;
-        case 128: hipLaunchKernelGGL((bwd_dkdv_kernel<128, T>), grid, dim3(kThreads), 0, s, a); break;
-        case 256: hipLaunchKernelGGL((bwd_dkdv_kernel<256, T>), grid, dim3(kThreads), 0, s, a); break;
+        case 16: return dkdv_launch<16, 4, 3, T>(a, num_kv_heads, s);
+        case 32: return dkdv_launch<32, 4, 3, T>(a, num_kv_heads, s);
+        case 64: return dkdv_launch<64, 4, 2, T>(a, num_kv_heads, s);
+        case 128: return dkdv_launch<128, 4, 2, T>(a, num_kv_heads, s);
+        case 256: return dkdv_launch<256, 2, 2, T>(a, num_kv_heads, s);
         default: return hipErrorInvalidValue;
     }
+}
+
+template <int D, int BN, int NW, int STAGES, typename T>
+hipError_t dq_launch(BwdArgs a, hipStream_t s) {
+    a.hpw = gcd_int(a.group, NW);
+    const int tpw = NW / a.hpw;
+    dim3 grid((a.seqlen_q + tpw * 32 - 1) / (tpw * 32), a.batch, a.num_heads / a.hpw);
+    hipLaunchKernelGGL((bwd_dq_kernel<D, BN, NW, STAGES, T>), grid, dim3(NW * 64), 0, s, a);
     return hipGetLastError();
 }
 
 template <typename T>
 hipError_t dq_dtype(const BwdArgs& a, int D, hipStream_t s) {
-    const int tpw = kWaves / a.hpw;
-    dim3 grid((a.seqlen_q + tpw * 32 - 1) / (tpw * 32), a.batch, a.num_heads / a.hpw);
     switch (D) {
-        case 16: hipLaunchKernelGGL((bwd_dq_kernel<16, 64, T>), grid, dim3(kThreads), 0, s, a); break;
-        case 32: hipLaunchKernelGGL((bwd_dq_kernel<32, 64, T>), grid, dim3(kThreads), 0, s, a); break;
-        case 64: hipLaunchKernelGGL((bwd_dq_kernel<64, 64, T>), grid, dim3(kThreads), 0, s, a); break;
-        case 128: hipLaunchKernelGGL((bwd_dq_kernel<128, 64, T>), grid, dim3(kThreads), 0, s, a); break;
-        case 256: hipLaunchKernelGGL((bwd_dq_kernel<256, 32, T>), grid, dim3(kThreads), 0, s, a); break;
+        case 16: return dq_launch<16, 64, 4, 4, T>(a, s);
+        case 32: return dq_launch<32, 64, 4, 4, T>(a, s);
+        case 64: return dq_launch<64, 64, 8, 4, T>(a, s);
+        case 128: return dq_launch<128, 64, 8, 3, T>(a, s);
+        case 256: return dq_launch<256, 32, 4, 3, T>(a, s);
         default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
 }
 
 }  // namespace

@@ -126,6 +126,107 @@ __device__ inline int perm32(int rho) { return (rho & ~12) | ((rho & 4) << 1) | 
 // Tile row held by output register r (0..15) of lane group g after the permuted load.
 __device__ inline int out_row32(int r, int g) { return 16 * (r >> 3) + 8 * g + (r & 7); }
 
+// ---- waits and barriers ---------------------------------------------------------------------
+// s_waitcnt immediates (gfx9 layout: vmcnt[3:0] + [15:14], expcnt[6:4], lgkmcnt[11:8]).
+template <int N>
+__device__ inline void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+__device__ inline void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14)); }
+// Workgroup barrier without the release/acquire fences of __syncthreads(), whose release
+// half would drain every in-flight load (vmcnt(0)) and defeat the asynchronous tile ring.
+// Callers order LDS themselves: all ds_read results are consumed before the barrier and
+// DMA tile loads are waited for with wait_vmcnt<>.
+__device__ inline void barrier_lds() {
+    wait_lgkmcnt0();
+    __builtin_amdgcn_s_barrier();
+}
+
+// ---- asynchronous tile ring (buffer_load ... lds) ---------------------------------------
+// Rows [n0, n0 + ROWS) x D of NT tensors (16-bit, row stride in elements) are fetched straight
+// into a swizzled LDS tile by buffer loads with the LDS destination: lane l of a load writes
+// 16 bytes at LDS base + 16 l, so each lane fetches the global chunk whose swizzled LDS slot is
+// that position. The buffer resource covers exactly the sequence's valid rows, so rows at or
+// beyond the length read as zero without touching memory. Each wave issues LOADS loads per
+// tile; completion is tracked per wave with wait_vmcnt and made workgroup-visible by a barrier.
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+// Raw buffer descriptor over [base, base + bytes): loads at offsets >= bytes return zero.
+__device__ inline i32x4 buffer_rsrc(const void* base, int64_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    // Wave-uniform by construction; readfirstlane places it in scalar registers as the buffer
+    // instructions require.
+    i32x4 r;
+    r[0] = __builtin_amdgcn_readfirstlane((int32_t)(uint32_t)(a & 0xffffffffu));
+    r[1] = __builtin_amdgcn_readfirstlane((int32_t)(uint32_t)((a >> 32) & 0xffffu));  // stride 0
+    r[2] = __builtin_amdgcn_readfirstlane((int32_t)(bytes > 0x7fffffff ? 0x7fffffff : bytes));
+    r[3] = 0x00020000;
+    return r;
+}
+// Descriptor over the valid rows [0, rows) of a (rows, D) 16-bit tensor with row stride tstride.
+__device__ inline i32x4 rows_rsrc(const uint16_t* base, int rows, int64_t tstride, int D) {
+    return buffer_rsrc(base, rows > 0 ? ((int64_t)(rows - 1) * tstride + D) * 2 : 0);
+}
+// LDS byte address of a pointer into __shared__ memory.
+__device__ inline uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)(p);
+}
+// buffer_load ... lds: every active lane fetches 16 (or 4) bytes at voff and the wave writes
+// them to LDS at lds_base + 16 (4) x lane. Issued through inline asm so the compiler does not
+// track these LDS writes: it would otherwise drain the load counter before every LDS
+// transpose read it cannot disambiguate. Completion is awaited explicitly (wait_vmcnt), and
+// no compiler-generated code in these kernels keeps a value in m0 across them.
+__device__ inline void dma16(i32x4 rsrc, uint32_t lds_base, uint32_t voff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(__builtin_amdgcn_readfirstlane(lds_base)), "v"(voff), "s"(rsrc)
+                 : "memory", "m0");
+}
+__device__ inline void dma4(i32x4 rsrc, uint32_t lds_base, uint32_t voff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+                 :
+                 : "s"(__builtin_amdgcn_readfirstlane(lds_base)), "v"(voff), "s"(rsrc)
+                 : "memory", "m0");
+}
+
+template <int D, int ROWS, int NT, int NW>
+struct TileRing {
+    static constexpr int CPR = D / 8;
+    static constexpr int LOADS_PER_TENSOR = ROWS * CPR / 64;  // 64-lane loads per tensor tile
+    static constexpr int LOADS = NT * LOADS_PER_TENSOR / NW;  // per wave per tile
+    static_assert((ROWS * CPR) % 64 == 0, "tile must be whole 64-lane loads");
+    static_assert((NT * LOADS_PER_TENSOR) % NW == 0, "loads must split evenly over the waves");
+
+    // tiles[t] = LDS tile of tensor t (ROWS * D elements); rsrc[t] / tstride_bytes[t] its source.
+    __device__ static inline void issue(const i32x4* rsrc, const int* tstride_bytes, uint16_t* const* tiles,
+                                        int n0, int wave, int lane) {
+#pragma unroll
+        for (int j = 0; j < LOADS; ++j) {
+            const int instr = wave * LOADS + j;
+            const int t = instr / LOADS_PER_TENSOR, within = instr % LOADS_PER_TENSOR;
+            const int p = within * 64 + lane;
+            const int row = p / CPR, phys = p % CPR;
+            const int logical = phys ^ lds_swz<D>(row);
+            const unsigned voff = (unsigned)((n0 + row) * tstride_bytes[t] + logical * 16);
+            dma16(rsrc[t], lds_addr(tiles[t] + within * 512), voff);
+        }
+    }
+};
+
+// Wait until the tile issued `ahead` tiles before the newest one has landed (this wave's part).
+template <int LOADS, int STAGES>
+__device__ inline void ring_wait(int tiles_after) {
+    // tiles_after = tiles issued after the awaited one, 0 .. STAGES - 2.
+    if (STAGES >= 4 && tiles_after >= 2) {
+        wait_vmcnt<(STAGES >= 4 ? 2 * LOADS : 0)>();
+    } else if (STAGES >= 3 && tiles_after >= 1) {
+        wait_vmcnt<(STAGES >= 3 ? LOADS : 0)>();
+    } else {
+        wait_vmcnt<0>();
+    }
+}
+
 // ---- sequences --------------------------------------------------------------------------
 
 struct SeqInfo {

@@ -74,7 +74,7 @@ __global__ __launch_bounds__(kThreads) void decode_splitk_kernel(DecodeArgs a) {
 
     const int split = blockIdx.x, b = blockIdx.y;
     const int kvh = blockIdx.z / a.row_tiles, rt = blockIdx.z % a.row_tiles;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int l16 = lane & 15, G = lane >> 4;
 
     const int L = seq_keys(a, b);

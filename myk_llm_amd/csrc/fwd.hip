@@ -38,52 +38,20 @@ struct FwdArgs {
     int hpw;         // query heads per workgroup
 };
 
-constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
-
 // Stage a BN x D tile (rows n0.., masked to < len) from global into a swizzled LDS tile.
-template <int D, int BN>
-struct TileLoader {
-    static constexpr int CPR = D / 8;
-    static constexpr int CHUNKS = BN * CPR;
-    static constexpr int PER = (CHUNKS + kThreads - 1) / kThreads;
-    s16x8 r[PER];
-
-    __device__ inline void load(const uint16_t* base, int64_t tstride, int n0, int len, int tid) {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            int idx = tid + i * kThreads;
-            int row = idx / CPR, ch = idx % CPR;
-            s16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
-            if ((CHUNKS % kThreads == 0 || idx < CHUNKS) && n0 + row < len)
-                v = ld16(base + (int64_t)(n0 + row) * tstride + ch * 8);
-            r[i] = v;
-        }
-    }
-    __device__ inline void store(uint16_t* lds, int tid) const {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            int idx = tid + i * kThreads;
-            if (CHUNKS % kThreads == 0 || idx < CHUNKS) {
-                int row = idx / CPR, ch = idx % CPR;
-                *reinterpret_cast<s16x8*>(lds + row * D + ((ch ^ lds_swz<D>(row)) << 3)) = r[i];
-            }
-        }
-    }
-};
-
-template <int D, int BN, typename T>
-__global__ __launch_bounds__(kThreads) void fwd_kernel(FwdArgs a) {
+template <int D, int BN, int NW, int STAGES, typename T>
+__global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdArgs a) {
     constexpr int KD = D / 16;            // k-steps of S^T = K Q^T
     constexpr int DB = (D + 31) / 32;     // 32-row blocks of O^T
     constexpr int NB = BN / 32;           // 32-key blocks per tile
     constexpr int KB = BN / 16;           // 16-key k-steps of O^T += V^T P^T
-    __shared__ __attribute__((aligned(16))) uint16_t smem[2][2][BN * D];
+    using Ring = TileRing<D, BN, 2, NW>;  // K and V tiles
+    __shared__ __attribute__((aligned(16))) uint16_t smem[STAGES][2][BN * D];
 
     const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int l32 = lane & 31, g = lane >> 5;
-    const int tpw = kWaves / a.hpw;
+    const int tpw = NW / a.hpw;
     const int mblk = gridDim.x - 1 - blockIdx.x;  // longest causal rows first (flash_attn.py:115)
     const int b = blockIdx.y;
     const int h_first = blockIdx.z * a.hpw;
@@ -118,11 +86,13 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(FwdArgs a) {
 
     const uint16_t* kbase = a.k + (int64_t)b * a.kbs + ks.tok0 * a.kts + (int64_t)kvh * a.khs;
     const uint16_t* vbase = a.v + (int64_t)b * a.vbs + ks.tok0 * a.vts + (int64_t)kvh * a.vhs;
+    const i32x4 rsrc[2] = {rows_rsrc(kbase, k_len, a.kts, D), rows_rsrc(vbase, k_len, a.vts, D)};
+    const int tstride[2] = {(int)(a.kts * 2), (int)(a.vts * 2)};
 
     // Q rows of this wave as the B operand of S^T = K Q^T: lane holds Q[s0 + l32][16kk + 8g + i].
     s16x8 qop[KD];
+    const int qi = s0 + l32;
     {
-        const int qi = s0 + l32;
         const uint16_t* qp = a.q + (int64_t)b * a.qbs + (qs.tok0 + qi) * a.qts + (int64_t)h * a.qhs;
 #pragma unroll
         for (int kk = 0; kk < KD; ++kk) {
@@ -131,6 +101,9 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(FwdArgs a) {
             qop[kk] = v;
         }
     }
+    // Q must have landed before the ring's loads join the same in-order counter; otherwise
+    // the compiler, unable to count loop-carried loads, drains the counter inside the loop.
+    wait_vmcnt<0>();
 
     f32x16 acc[DB];
 #pragma unroll
@@ -138,106 +111,99 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(FwdArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
     float m_i = kNegFloor, l_i = 0.f;
-    const int qi = s0 + l32;
 
-    TileLoader<D, BN> kl, vl;
-    if (wg_hi > wg_lo) {
-        kl.load(kbase, a.kts, wg_lo, k_len, tid);
-        vl.load(vbase, a.vts, wg_lo, k_len, tid);
-        kl.store(smem[0][0], tid);
-        vl.store(smem[0][1], tid);
-    }
-    int buf = 0;
-    for (int n0 = wg_lo; n0 < wg_hi; n0 += BN) {
-        __syncthreads();
-        const bool more = n0 + BN < wg_hi;
-        if (more) {
-            kl.load(kbase, a.kts, n0 + BN, k_len, tid);
-            vl.load(vbase, a.vts, n0 + BN, k_len, tid);
-        }
+    const int ntiles = wg_hi > wg_lo ? (wg_hi - wg_lo + BN - 1) / BN : 0;
+    auto issue = [&](int t) {
+        uint16_t* tiles[2] = {smem[t % STAGES][0], smem[t % STAGES][1]};
+        Ring::issue(rsrc, tstride, tiles, wg_lo + t * BN, wave, lane);
+    };
+#pragma unroll
+    for (int t = 0; t < STAGES - 1; ++t)
+        if (t < ntiles) issue(t);
+
+    for (int t = 0; t < ntiles; ++t) {
+        const int n0 = wg_lo + t * BN;
+        const int after = ntiles - 1 - t < STAGES - 2 ? ntiles - 1 - t : STAGES - 2;
+        ring_wait<Ring::LOADS, STAGES>(after);
+        barrier_lds();  // tile t landed for every wave; tile t - 1's stage is free again
+        if (t + STAGES - 1 < ntiles) issue(t + STAGES - 1);
         const bool active = bs > 0 && n0 < wr.hi && n0 + BN > wr.lo;
-        if (active) {
-            const bool masked = !(n0 >= wr.mid_lo && n0 + BN <= wr.mid_hi);
-            const uint16_t* Ks = smem[buf][0];
-            const uint16_t* Vs = smem[buf][1];
-            // S^T = K Q^T, 32 keys per block.
-            f32x16 st[NB];
+        if (!active) continue;
+        const bool masked = !(n0 >= wr.mid_lo && n0 + BN <= wr.mid_hi);
+        const uint16_t* Ks = smem[t % STAGES][0];
+        const uint16_t* Vs = smem[t % STAGES][1];
+        // S^T = K Q^T, 32 keys per block.
+        f32x16 st[NB];
 #pragma unroll
-            for (int nb = 0; nb < NB; ++nb) {
+        for (int nb = 0; nb < NB; ++nb) {
 #pragma unroll
-                for (int r = 0; r < 16; ++r) st[nb][r] = 0.f;
-                const int row = nb * 32 + perm32(l32);
+            for (int r = 0; r < 16; ++r) st[nb][r] = 0.f;
+            const int row = nb * 32 + perm32(l32);
 #pragma unroll
-                for (int kk = 0; kk < KD; ++kk) {
-                    s16x8 kop = *reinterpret_cast<const s16x8*>(Ks + row * D + (((2 * kk + g) ^ lds_swz<D>(row)) << 3));
-                    st[nb] = T::mfma32(kop, qop[kk], st[nb]);
-                }
-            }
-            // Online softmax (flash_attn.py:90-96) on scaled scores.
-            float mx = kNegFloor;
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    float x = st[nb][r] * a.qk_scale;
-                    if (masked) {
-                        const int key = n0 + nb * 32 + out_row32(r, g);
-                        const int rel = key - qi;
-                        const bool vis = rel >= lo_off && rel <= hi_off && key < k_len;
-                        x = vis ? x : -INFINITY;
-                    }
-                    st[nb][r] = x;
-                    mx = fmaxf(mx, x);
-                }
-            mx = max_halves(mx);
-            const float m_new = fmaxf(m_i, mx);
-            const float alpha = fast_exp2(m_i - m_new);
-            float lsum = 0.f;
-            s16x8 pop[KB];
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-                for (int half = 0; half < 2; ++half) {
-                    uint32_t w[4];
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        float p0 = fast_exp2(st[nb][8 * half + 2 * i] - m_new);
-                        float p1 = fast_exp2(st[nb][8 * half + 2 * i + 1] - m_new);
-                        lsum += p0 + p1;
-                        w[i] = T::pack2(p0, p1);
-                    }
-                    u32x4 wv = {w[0], w[1], w[2], w[3]};
-                    pop[nb * 2 + half] = __builtin_bit_cast(s16x8, wv);
-                }
-            l_i = l_i * alpha + lsum;
-            m_i = m_new;
-#pragma unroll
-            for (int db = 0; db < DB; ++db)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
-            // O^T += V^T P^T; V^T operand through the LDS transpose read.
-            const int G = lane >> 4, jj = lane & 15;
-#pragma unroll
-            for (int db = 0; db < DB; ++db) {
-                int col = 32 * db + 16 * (G & 1) + 4 * (jj & 3);
-                const bool dvalid = col < D;
-                if (!dvalid) col = col % D;
-#pragma unroll
-                for (int kb = 0; kb < KB; ++kb) {
-                    const int row = 16 * kb + 8 * (G >> 1) + (jj >> 2);
-                    s16x4 lo4 = ds_read_tr(Vs + lds_off<D>(row, col));
-                    s16x4 hi4 = ds_read_tr(Vs + lds_off<D>(row + 4, col));
-                    s16x8 vop = cat4(lo4, hi4);
-                    if (!dvalid) vop = s16x8{0, 0, 0, 0, 0, 0, 0, 0};
-                    acc[db] = T::mfma32(vop, pop[kb], acc[db]);
-                }
+            for (int kk = 0; kk < KD; ++kk) {
+                s16x8 kop = *reinterpret_cast<const s16x8*>(Ks + row * D + (((2 * kk + g) ^ lds_swz<D>(row)) << 3));
+                st[nb] = T::mfma32(kop, qop[kk], st[nb]);
             }
         }
-        if (more) {
-            kl.store(smem[buf ^ 1][0], tid);
-            vl.store(smem[buf ^ 1][1], tid);
+        // Online softmax (flash_attn.py:90-96) on scaled scores.
+        float mx = kNegFloor;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                float x = st[nb][r] * a.qk_scale;
+                if (masked) {
+                    const int key = n0 + nb * 32 + out_row32(r, g);
+                    const int rel = key - qi;
+                    const bool vis = rel >= lo_off && rel <= hi_off && key < k_len;
+                    x = vis ? x : -INFINITY;
+                }
+                st[nb][r] = x;
+                mx = fmaxf(mx, x);
+            }
+        mx = max_halves(mx);
+        const float m_new = fmaxf(m_i, mx);
+        const float alpha = fast_exp2(m_i - m_new);
+        float lsum = 0.f;
+        s16x8 pop[KB];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                uint32_t w[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float p0 = fast_exp2(st[nb][8 * half + 2 * i] - m_new);
+                    float p1 = fast_exp2(st[nb][8 * half + 2 * i + 1] - m_new);
+                    lsum += p0 + p1;
+                    w[i] = T::pack2(p0, p1);
+                }
+                u32x4 wv = {w[0], w[1], w[2], w[3]};
+                pop[nb * 2 + half] = __builtin_bit_cast(s16x8, wv);
+            }
+        l_i = l_i * alpha + lsum;
+        m_i = m_new;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
+        // O^T += V^T P^T; V^T operand through the LDS transpose read.
+        const int G = lane >> 4, jj = lane & 15;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+            int col = 32 * db + 16 * (G & 1) + 4 * (jj & 3);
+            const bool dvalid = col < D;
+            if (!dvalid) col = col % D;
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+                const int row = 16 * kb + 8 * (G >> 1) + (jj >> 2);
+                s16x4 lo4 = ds_read_tr(Vs + lds_off<D>(row, col));
+                s16x4 hi4 = ds_read_tr(Vs + lds_off<D>(row + 4, col));
+                s16x8 vop = cat4(lo4, hi4);
+                if (!dvalid) vop = s16x8{0, 0, 0, 0, 0, 0, 0, 0};
+                acc[db] = T::mfma32(vop, pop[kb], acc[db]);
+            }
         }
-        buf ^= 1;
     }
 
     if (bs <= 0) return;
@@ -271,23 +237,25 @@ int gcd_int(int x, int y) {
     return x;
 }
 
-template <int D, int BN, typename T>
-hipError_t launch_typed(const FwdArgs& args, int batch, int num_heads, int max_q, hipStream_t s) {
-    const int tpw = kWaves / args.hpw;
+template <int D, int BN, int NW, int STAGES, typename T>
+hipError_t launch_typed(FwdArgs args, int batch, int num_heads, int max_q, hipStream_t s) {
+    args.hpw = gcd_int(args.group, NW);
+    const int tpw = NW / args.hpw;
     dim3 grid((max_q + tpw * 32 - 1) / (tpw * 32), batch, num_heads / args.hpw);
     if (grid.x == 0 || batch == 0) return hipSuccess;
-    hipLaunchKernelGGL((fwd_kernel<D, BN, T>), grid, dim3(kThreads), 0, s, args);
+    hipLaunchKernelGGL((fwd_kernel<D, BN, NW, STAGES, T>), grid, dim3(NW * 64), 0, s, args);
     return hipGetLastError();
 }
 
+// Tile shapes per head_dim: (keys per tile, waves per workgroup, LDS ring stages).
 template <typename T>
 hipError_t launch_dtype(const FwdArgs& args, int D, int batch, int num_heads, int max_q, hipStream_t s) {
     switch (D) {
-        case 16: return launch_typed<16, 64, T>(args, batch, num_heads, max_q, s);
-        case 32: return launch_typed<32, 64, T>(args, batch, num_heads, max_q, s);
-        case 64: return launch_typed<64, 64, T>(args, batch, num_heads, max_q, s);
-        case 128: return launch_typed<128, 64, T>(args, batch, num_heads, max_q, s);
-        case 256: return launch_typed<256, 32, T>(args, batch, num_heads, max_q, s);
+        case 16: return launch_typed<16, 64, 4, 4, T>(args, batch, num_heads, max_q, s);
+        case 32: return launch_typed<32, 64, 4, 4, T>(args, batch, num_heads, max_q, s);
+        case 64: return launch_typed<64, 64, 8, 4, T>(args, batch, num_heads, max_q, s);
+        case 128: return launch_typed<128, 64, 8, 3, T>(args, batch, num_heads, max_q, s);
+        case 256: return launch_typed<256, 32, 4, 3, T>(args, batch, num_heads, max_q, s);
         default: return hipErrorInvalidValue;
     }
 }
@@ -315,7 +283,7 @@ hipError_t launch_fwd(const mykfa_fwd_params& p, hipStream_t stream) {
     a.wr = p.window_right;
     a.qk_scale = p.softmax_scale * 1.4426950408889634f;
     a.group = p.num_heads / p.num_kv_heads;
-    a.hpw = gcd_int(a.group, kWaves);
+    a.hpw = 1;  // set per tile shape in launch_typed
     if (p.dtype == MYKFA_BF16) return launch_dtype<BF16>(a, p.head_dim, p.batch, p.num_heads, p.max_seqlen_q, stream);
     return launch_dtype<FP16>(a, p.head_dim, p.batch, p.num_heads, p.max_seqlen_q, stream);
 }

@@ -291,10 +291,13 @@ class _FlashAttn(torch.autograd.Function):
         ctx.save_for_backward(q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k)
         ctx.args = (max_seqlen_q, max_seqlen_k, softmax_scale, window_left, window_right)
         ctx.mark_non_differentiable(lse)
+        ctx.set_materialize_grads(False)  # no zero-filled gradient for the lse output
         return out, lse
 
     @staticmethod
     def backward(ctx, dout, dlse):  # pyright: ignore[reportIncompatibleMethodOverride]
+        if dout is None:
+            return (None,) * 10
         q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k = ctx.saved_tensors
         dq, dk, dv = _bwd(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, *ctx.args)
         return dq, dk, dv, None, None, None, None, None, None, None

@@ -1,0 +1,130 @@
+"""Split-K decode and KV append on the GPU: every split count agrees with the oracle, the
+cache write is bit-exact (tests/test_flash_attn.py:102), writes beyond the capacity are
+dropped, and a HIP-graph capture of flash_attn_with_kvcache replays to the eager result
+(the static-cache decode caller captures one step, scripts/benchmark_decode.py:149-151)."""
+
+import ctypes
+import sys
+
+import pytest
+import torch
+
+from _util import assert_close, assert_lse
+from myk_llm_amd import _lib, flash_attn_with_kvcache
+from myk_llm_amd import flash_attn as fa
+from oracle.attention import kvcache_reference
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def _make(batch, cap, lens, nq, heads, kv_heads, d, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    kc = torch.randn(batch, cap, kv_heads, d, generator=g).to(torch.bfloat16)
+    vc = torch.randn(batch, cap, kv_heads, d, generator=g).to(torch.bfloat16)
+    q = torch.randn(batch, nq, heads, d, generator=g).to(torch.bfloat16)
+    kn = torch.randn(batch, nq, kv_heads, d, generator=g).to(torch.bfloat16)
+    vn = torch.randn(batch, nq, kv_heads, d, generator=g).to(torch.bfloat16)
+    return q, kc, vc, kn, vn, torch.tensor(lens, dtype=torch.int32)
+
+
+@pytest.mark.parametrize("nq", [1, 2, 4, 16])
+@pytest.mark.parametrize("heads, kv_heads", [(16, 4), (8, 8), (8, 1)])
+@pytest.mark.parametrize("window", [(-1, -1), (100, 0)])
+def test_decode_matches_oracle(nq, heads, kv_heads, window):
+    _say(f"decode nq={nq} H={heads}/{kv_heads} window={window}")
+    lens = [0, 1, 31, 32, 33, 500, 1000, 2047]
+    q, kc, vc, kn, vn, cl = _make(len(lens), 2100, lens, nq, heads, kv_heads, 64)
+    exp, exp_lse, ekc, evc = kvcache_reference(q.float(), kc.float(), vc.float(), kn.float(), vn.float(), cl, True,
+                                               window)
+    kcg, vcg = kc.cuda(), vc.cuda()
+    out, lse = flash_attn_with_kvcache(q.cuda(), kcg, vcg, kn.cuda(), vn.cuda(), cache_seqlens=cl.cuda(),
+                                       causal=True, window_size=window, return_softmax_lse=True)
+    torch.cuda.synchronize()
+    assert torch.equal(kcg.cpu().float(), ekc) and torch.equal(vcg.cpu().float(), evc)
+    assert_close(out, exp)
+    assert_lse(lse, exp_lse)
+
+
+@pytest.mark.parametrize("d", [16, 32, 64, 128, 256])
+def test_decode_head_dims(d):
+    _say(f"decode D={d}")
+    lens = [7, 300, 129]
+    q, kc, vc, kn, vn, cl = _make(3, 400, lens, 4, 8, 2, d, seed=1)
+    exp, exp_lse, _, _ = kvcache_reference(q.float(), kc.float(), vc.float(), kn.float(), vn.float(), cl, True,
+                                           (-1, -1))
+    out, lse = flash_attn_with_kvcache(q.cuda(), kc.cuda(), vc.cuda(), kn.cuda(), vn.cuda(), cache_seqlens=cl.cuda(),
+                                       causal=True, return_softmax_lse=True)
+    assert_close(out, exp)
+    assert_lse(lse, exp_lse)
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 7, 16, 64])
+def test_every_split_count_agrees(splits):
+    """The C ABI with an explicit split count: split-K + merge is independent of the split."""
+    _say(f"splits={splits}")
+    lens = [1000, 17, 4000, 2500]
+    q, kc, vc, _, _, cl = _make(len(lens), 4096, lens, 4, 16, 4, 64, seed=2)
+    exp, exp_lse, _, _ = kvcache_reference(q.float(), kc.float(), vc.float(), None, None, cl, True, (-1, -1))
+    qg, kcg, vcg, clg = q.cuda(), kc.cuda(), vc.cuda(), cl.cuda()
+    out = torch.empty_like(qg)
+    lse = torch.empty((qg.shape[2], qg.shape[0] * qg.shape[1]), dtype=torch.float32, device="cuda")
+    p = _lib.DecodeParams()
+    p.fwd = fa._fwd_params(qg, kcg, vcg, out, lse, None, None, clg, q.shape[1], kc.shape[1], 0.125,
+                           _lib.UNBOUNDED, 0)
+    p.num_splits = splits
+    L = _lib.lib()
+    nbytes = L.mykfa_decode_workspace_size(p.fwd.batch, p.fwd.num_heads, p.fwd.max_seqlen_q, 64, splits)
+    ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    _lib.check(L.mykfa_decode(ctypes.byref(p), ws.data_ptr(), ws.numel(), stream))
+    torch.cuda.synchronize()
+    assert_close(out, exp)
+    assert_lse(lse, exp_lse)
+    # Too small a workspace is rejected before any launch.
+    if nbytes > 0:
+        assert L.mykfa_decode(ctypes.byref(p), ws.data_ptr(), nbytes - 1, stream) == _lib.ERR_WORKSPACE
+
+
+def test_append_beyond_capacity_is_dropped():
+    b, cap, hk, d = 2, 10, 2, 64
+    kc = torch.zeros(b, cap, hk, d, dtype=torch.bfloat16, device="cuda")
+    vc = torch.zeros_like(kc)
+    kn = torch.randn(b, 4, hk, d).to(torch.bfloat16).cuda()
+    vn = torch.randn(b, 4, hk, d).to(torch.bfloat16).cuda()
+    q = torch.randn(b, 4, 4, d).to(torch.bfloat16).cuda()
+    cl = torch.tensor([2, 8], dtype=torch.int32, device="cuda")
+    flash_attn_with_kvcache(q, kc, vc, kn, vn, cache_seqlens=cl, causal=True)
+    assert torch.equal(kc[0, 2:6], kn[0]) and torch.equal(kc[1, 8:10], kn[1, :2])
+    assert torch.all(kc[0, 6:] == 0) and torch.all(kc[0, :2] == 0)
+
+
+def test_graph_capture_replays_match_eager():
+    """Capture one decode step (append + split-K + merge) in a HIP graph; several replays with
+    eager work and syncs in between all reproduce the eager result bit for bit."""
+    lens = [100, 900, 33]
+    q, kc, vc, kn, vn, cl = _make(3, 1024, lens, 4, 16, 4, 64, seed=3)
+    q, kn, vn, cl = q.cuda(), kn.cuda(), vn.cuda(), cl.cuda()
+    kc_e, vc_e = kc.cuda(), vc.cuda()
+    eager = flash_attn_with_kvcache(q, kc_e, vc_e, kn, vn, cache_seqlens=cl, causal=True).clone()
+    kc_g, vc_g = kc.cuda(), vc.cuda()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        flash_attn_with_kvcache(q, kc_g, vc_g, kn, vn, cache_seqlens=cl, causal=True)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = flash_attn_with_kvcache(q, kc_g, vc_g, kn, vn, cache_seqlens=cl, causal=True)
+    for i in range(4):
+        out.zero_()
+        torch.randn(1000, device="cuda").sum()  # unrelated eager work between replays
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+    assert torch.equal(kc_g, kc_e)
