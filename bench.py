@@ -259,6 +259,9 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only: no other configs, no CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager calls instead of graph replays")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run a plain 256 MiB fp32 copy kernel 3 times (reads and writes 2^28 bytes "
+                         "each), the reference dispatch for scaling FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for {args.gpus}); "
@@ -268,6 +271,13 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
     _lib.lib()
+    if args.copy_calibration:
+        src = torch.randn(1 << 26, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.mul(src, 1.0, out=dst)  # one elementwise kernel: 256 MiB read, 256 MiB written
+        torch.cuda.synchronize()
+        del src, dst
     W = workloads()
     w = W[args.workload]
     log(f"headline {w.name}: fwd+bwd, steps={args.steps} warmup={args.warmup}")

@@ -42,6 +42,7 @@ struct BwdArgs {
     int hpw;
     int num_heads;
     int batch;
+    int gx, gy, gz;  // logical grid (fastest first), XCD-grouped by the launchers
 };
 
 // ---- 1. delta = rowsum(dO * O) ---------------------------------------------------------
@@ -117,8 +118,12 @@ __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
     const int l32 = lane & 31, g = lane >> 5;
     const int hpw = a.hpw, kpw = NW / hpw;
     const int kb_w = wave / hpw, hs = wave % hpw;
-    const int n0 = blockIdx.x * 32 * kpw;  // causal: the first key blocks see the most queries
-    const int b = blockIdx.y, kvh = blockIdx.z;
+    // Logical block: key block fastest, then KV head, then sequence (XCD-grouped).
+    const int logical = xcd_logical(blockIdx.x);
+    if (logical >= a.gx * a.gy * a.gz) return;
+    const int n0 = (logical % a.gx) * 32 * kpw;  // causal: the first key blocks see the most queries
+    const int kvh = (logical / a.gx) % a.gz;
+    const int b = logical / (a.gx * a.gz);
     SeqInfo ks = seq_info(b, a.cu_k, nullptr, a.seqlen_k, false);
     const int k_len = ks.len;
     if (n0 >= k_len) return;
@@ -313,9 +318,12 @@ __global__ __launch_bounds__(NW * 64) void bwd_dq_kernel(BwdArgs a) {
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int l32 = lane & 31, g = lane >> 5;
     const int tpw = NW / a.hpw;
-    const int mblk = gridDim.x - 1 - blockIdx.x;
-    const int b = blockIdx.y;
-    const int h_first = blockIdx.z * a.hpw;
+    // Logical block: query block fastest (longest rows first), then head group, then sequence.
+    const int logical = xcd_logical(blockIdx.x);
+    if (logical >= a.gx * a.gy * a.gz) return;
+    const int mblk = a.gx - 1 - logical % a.gx;
+    const int h_first = (logical / a.gx) % a.gz * a.hpw;
+    const int b = logical / (a.gx * a.gz);
     SeqInfo qs = seq_info(b, a.cu_q, nullptr, a.seqlen_q, false);
     const int tok_base = mblk * tpw * 32;
     if (tok_base >= qs.len) return;
@@ -513,8 +521,13 @@ template <int D, int NW, int STAGES, typename T>
 hipError_t dkdv_launch(BwdArgs a, int num_kv_heads, hipStream_t s) {
     a.hpw = gcd_int(a.group, NW);
     const int keys_per_wg = 32 * (NW / a.hpw);
-    dim3 grid((a.seqlen_k + keys_per_wg - 1) / keys_per_wg, a.batch, num_kv_heads);
-    hipLaunchKernelGGL((bwd_dkdv_kernel<D, NW, STAGES, T>), grid, dim3(NW * 64), 0, s, a);
+    a.gx = (a.seqlen_k + keys_per_wg - 1) / keys_per_wg;
+    a.gy = a.batch;
+    a.gz = num_kv_heads;
+    const long long n = (long long)a.gx * a.gy * a.gz;
+    if (n == 0) return hipSuccess;
+    if (n > (1LL << 30)) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL((bwd_dkdv_kernel<D, NW, STAGES, T>), dim3(xcd_grid((int)n)), dim3(NW * 64), 0, s, a);
     return hipGetLastError();
 }
 
@@ -534,8 +547,13 @@ template <int D, int BN, int NW, int STAGES, typename T>
 hipError_t dq_launch(BwdArgs a, hipStream_t s) {
     a.hpw = gcd_int(a.group, NW);
     const int tpw = NW / a.hpw;
-    dim3 grid((a.seqlen_q + tpw * 32 - 1) / (tpw * 32), a.batch, a.num_heads / a.hpw);
-    hipLaunchKernelGGL((bwd_dq_kernel<D, BN, NW, STAGES, T>), grid, dim3(NW * 64), 0, s, a);
+    a.gx = (a.seqlen_q + tpw * 32 - 1) / (tpw * 32);
+    a.gy = a.batch;
+    a.gz = a.num_heads / a.hpw;
+    const long long n = (long long)a.gx * a.gy * a.gz;
+    if (n == 0) return hipSuccess;
+    if (n > (1LL << 30)) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL((bwd_dq_kernel<D, BN, NW, STAGES, T>), dim3(xcd_grid((int)n)), dim3(NW * 64), 0, s, a);
     return hipGetLastError();
 }
 

@@ -227,6 +227,23 @@ __device__ inline void ring_wait(int tiles_after) {
     }
 }
 
+// ---- XCD-aware workgroup order ------------------------------------------------------------
+// MI355X has 8 XCDs, each with its own L2; the dispatcher deals workgroup i to XCD i % 8. The
+// launchers pad a 1-D grid to a multiple of 8 * kXcdChunk and each workgroup maps its id to a
+// logical block so that every run of kXcdChunk consecutive logical blocks (neighbouring
+// query / key blocks of one head, which read the same K/V or Q/dO tiles) executes on one XCD
+// and shares its L2. Logical ids >= n (padding) exit at once.
+constexpr int kXcds = 8;
+constexpr int kXcdChunk = 8;
+__host__ __device__ inline int xcd_grid(int n) {
+    const int q = kXcds * kXcdChunk;
+    return (n + q - 1) / q * q;
+}
+__device__ inline int xcd_logical(int pid) {
+    const int xcd = pid % kXcds, slot = pid / kXcds;
+    return ((slot / kXcdChunk) * kXcds + xcd) * kXcdChunk + slot % kXcdChunk;
+}
+
 // ---- sequences --------------------------------------------------------------------------
 
 struct SeqInfo {

@@ -36,6 +36,7 @@ struct FwdArgs {
     float qk_scale;  // softmax_scale * log2(e)  (flash_attn.py:368)
     int group;       // num_heads / num_kv_heads
     int hpw;         // query heads per workgroup
+    int gx, gy, gz;  // logical grid: query blocks x sequences x head groups
 };
 
 // Stage a BN x D tile (rows n0.., masked to < len) from global into a swizzled LDS tile.
@@ -52,9 +53,12 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int l32 = lane & 31, g = lane >> 5;
     const int tpw = NW / a.hpw;
-    const int mblk = gridDim.x - 1 - blockIdx.x;  // longest causal rows first (flash_attn.py:115)
-    const int b = blockIdx.y;
-    const int h_first = blockIdx.z * a.hpw;
+    // Logical block (query block fastest, then head group, then sequence), XCD-grouped.
+    const int logical = xcd_logical(blockIdx.x);
+    if (logical >= a.gx * a.gy * a.gz) return;
+    const int mblk = a.gx - 1 - logical % a.gx;  // longest causal rows first (flash_attn.py:115)
+    const int h_first = (logical / a.gx) % a.gz * a.hpw;
+    const int b = logical / (a.gx * a.gz);
 
     SeqInfo qs = seq_info(b, a.cu_q, nullptr, a.seqlen_q, false);
     const int tok_base = mblk * tpw * 32;
@@ -241,9 +245,13 @@ template <int D, int BN, int NW, int STAGES, typename T>
 hipError_t launch_typed(FwdArgs args, int batch, int num_heads, int max_q, hipStream_t s) {
     args.hpw = gcd_int(args.group, NW);
     const int tpw = NW / args.hpw;
-    dim3 grid((max_q + tpw * 32 - 1) / (tpw * 32), batch, num_heads / args.hpw);
-    if (grid.x == 0 || batch == 0) return hipSuccess;
-    hipLaunchKernelGGL((fwd_kernel<D, BN, NW, STAGES, T>), grid, dim3(NW * 64), 0, s, args);
+    args.gx = (max_q + tpw * 32 - 1) / (tpw * 32);
+    args.gy = batch;
+    args.gz = num_heads / args.hpw;
+    const long long n = (long long)args.gx * args.gy * args.gz;
+    if (n == 0) return hipSuccess;
+    if (n > (1LL << 30)) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL((fwd_kernel<D, BN, NW, STAGES, T>), dim3(xcd_grid((int)n)), dim3(NW * 64), 0, s, args);
     return hipGetLastError();
 }
 
