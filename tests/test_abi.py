@@ -1,0 +1,163 @@
+"""The C-ABI library on the CPU: it loads without a GPU, exports every symbol include/mykfa.h
+declares, its struct layouts match the ctypes mirror, and its host-only validation returns
+each documented status code (flash_attn.py:336-346, :476-477) without touching a device."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from myk_llm_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "mykfa.h"
+
+
+@pytest.fixture(scope="module")
+def L():
+    return _lib.lib()
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(mykfa_\w+)\s*\(", text, re.M)))
+
+
+def test_every_declared_symbol_is_exported_and_bound(L):
+    names = declared_functions()
+    assert len(names) >= 20
+    for name in names:
+        assert hasattr(L, name), f"{name} missing from libmykfa.so"
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+    assert set(_lib.SIGNATURES) == set(names)
+
+
+def test_version_and_struct_sizes(L):
+    assert L.mykfa_abi_version() == 1
+    assert b"gfx950" in L.mykfa_version()
+    assert L.mykfa_sizeof_fwd_params() == ctypes.sizeof(_lib.FwdParams)
+    assert L.mykfa_sizeof_bwd_params() == ctypes.sizeof(_lib.BwdParams)
+    assert L.mykfa_sizeof_decode_params() == ctypes.sizeof(_lib.DecodeParams)
+    assert L.mykfa_sizeof_kv_append_params() == ctypes.sizeof(_lib.KvAppendParams)
+
+
+def good_fwd():
+    p = _lib.FwdParams()
+    p.q = p.k = p.v = p.o = p.lse = 0x10000  # aligned dummies: validation never dereferences
+    p.q_batch_stride, p.q_token_stride, p.q_head_stride = 128 * 8 * 64, 8 * 64, 64
+    p.k_batch_stride, p.k_token_stride, p.k_head_stride = 128 * 2 * 64, 2 * 64, 64
+    p.v_batch_stride, p.v_token_stride, p.v_head_stride = 128 * 2 * 64, 2 * 64, 64
+    p.o_batch_stride, p.o_token_stride, p.o_head_stride = 128 * 8 * 64, 8 * 64, 64
+    p.lse_head_stride = 2 * 128
+    p.batch, p.num_heads, p.num_kv_heads, p.head_dim = 2, 8, 2, 64
+    p.max_seqlen_q = p.max_seqlen_k = 128
+    p.window_left, p.window_right = _lib.UNBOUNDED, 0
+    p.softmax_scale = 0.125
+    p.dtype = _lib.DTYPE_BF16
+    return p
+
+
+def test_valid_forward_params_pass(L):
+    assert L.mykfa_validate_fwd(ctypes.byref(good_fwd())) == _lib.OK
+    assert L.mykfa_last_error() == b""
+
+
+@pytest.mark.parametrize("field, value, code, text", [
+    ("dtype", 7, _lib.ERR_UNSUPPORTED, b"bf16"),
+    ("head_dim", 48, _lib.ERR_UNSUPPORTED, b"head_dim"),
+    ("num_kv_heads", 3, _lib.ERR_INVALID, b"multiple"),
+    ("num_heads", 0, _lib.ERR_INVALID, b"multiple"),
+    ("batch", -1, _lib.ERR_INVALID, b"negative"),
+    ("window_left", -1, _lib.ERR_INVALID, b"window"),
+    ("q", 0, _lib.ERR_INVALID, b"q is NULL"),
+    ("q", 0x10008, _lib.ERR_INVALID, b"16-byte aligned"),
+    ("k_token_stride", 2 * 64 + 4, _lib.ERR_INVALID, b"multiples of 8"),
+    ("lse", 0, _lib.ERR_INVALID, b"lse is NULL"),
+    ("lse_head_stride", 10, _lib.ERR_INVALID, b"lse_head_stride"),
+    ("softmax_scale", float("nan"), _lib.ERR_INVALID, b"NaN"),
+])
+def test_forward_validation_errors(L, field, value, code, text):
+    p = good_fwd()
+    setattr(p, field, value)
+    assert L.mykfa_validate_fwd(ctypes.byref(p)) == code
+    assert text in L.mykfa_last_error()
+    # The launching entry point rejects the same input before any HIP call.
+    assert L.mykfa_fwd(ctypes.byref(p), None) == code
+
+
+def test_varlen_rules(L):
+    p = good_fwd()
+    p.cu_seqlens_q = 0x20000
+    assert L.mykfa_validate_fwd(ctypes.byref(p)) == _lib.ERR_INVALID  # only one cu_seqlens
+    p.cu_seqlens_k = 0x20000
+    assert L.mykfa_validate_fwd(ctypes.byref(p)) == _lib.ERR_INVALID  # batch strides must be 0
+    p.q_batch_stride = p.k_batch_stride = p.v_batch_stride = p.o_batch_stride = 0
+    assert L.mykfa_validate_fwd(ctypes.byref(p)) == _lib.OK
+    p.seqused_k = 0x30000
+    assert L.mykfa_validate_fwd(ctypes.byref(p)) == _lib.ERR_INVALID
+
+
+def test_empty_problems_succeed_without_a_device(L):
+    p = good_fwd()
+    p.batch = 0
+    assert L.mykfa_fwd(ctypes.byref(p), None) == _lib.OK
+    p = good_fwd()
+    p.max_seqlen_q = 0
+    assert L.mykfa_fwd(ctypes.byref(p), None) == _lib.OK
+
+
+def test_backward_and_decode_validation(L):
+    b = _lib.BwdParams()
+    b.fwd = good_fwd()
+    assert L.mykfa_validate_bwd(ctypes.byref(b)) == _lib.ERR_INVALID  # dout NULL
+    b.dout = b.dq = b.dk = b.dv = b.delta = 0x40000
+    for pre in ("do", "dq"):
+        setattr(b, f"{pre}_batch_stride", 128 * 8 * 64)
+        setattr(b, f"{pre}_token_stride", 8 * 64)
+        setattr(b, f"{pre}_head_stride", 64)
+    for pre in ("dk", "dv"):
+        setattr(b, f"{pre}_batch_stride", 128 * 2 * 64)
+        setattr(b, f"{pre}_token_stride", 2 * 64)
+        setattr(b, f"{pre}_head_stride", 64)
+    assert L.mykfa_validate_bwd(ctypes.byref(b)) == _lib.OK
+    b.fwd.seqused_k = 0x50000
+    assert L.mykfa_validate_bwd(ctypes.byref(b)) == _lib.ERR_INVALID
+
+    d = _lib.DecodeParams()
+    d.fwd = good_fwd()
+    d.num_splits = 0
+    assert L.mykfa_validate_decode(ctypes.byref(d)) == _lib.OK
+    d.num_splits = 5000
+    assert L.mykfa_validate_decode(ctypes.byref(d)) == _lib.ERR_INVALID
+    d.num_splits = 4
+    need = L.mykfa_decode_workspace_size(2, 8, 128, 64, 4)
+    assert need == 4 * 2 * 8 * 128 * (64 + 1) * 4
+    assert L.mykfa_decode_workspace_size(2, 8, 128, 64, 1) == 0  # one split writes o/lse directly
+    assert L.mykfa_decode(ctypes.byref(d), None, 0, None) == _lib.ERR_WORKSPACE
+
+
+def test_decode_split_heuristic(L):
+    assert L.mykfa_decode_num_splits(64, 4, 16388) >= 8  # fills the chip with 256 (seq, head) pairs
+    assert L.mykfa_decode_num_splits(1, 1, 100) == 1  # short caches are not split
+    for b, h, c in [(1, 1, 1 << 20), (512, 8, 4096), (64, 4, 256)]:
+        s = L.mykfa_decode_num_splits(b, h, c)
+        assert 1 <= s <= 1024
+
+
+def test_kv_append_validation(L):
+    p = _lib.KvAppendParams()
+    p.batch, p.seqlen_new, p.capacity, p.num_kv_heads, p.head_dim, p.dtype = 2, 1, 16, 2, 64, _lib.DTYPE_BF16
+    assert L.mykfa_validate_kv_append(ctypes.byref(p)) == _lib.ERR_INVALID  # cache_seqlens NULL
+    p.cache_seqlens = 0x1000
+    assert L.mykfa_validate_kv_append(ctypes.byref(p)) == _lib.ERR_INVALID  # k_cache NULL
+    p.k_cache = p.v_cache = p.k_new = p.v_new = 0x2000
+    assert L.mykfa_validate_kv_append(ctypes.byref(p)) == _lib.OK
+    p.head_dim = 40
+    assert L.mykfa_validate_kv_append(ctypes.byref(p)) == _lib.ERR_UNSUPPORTED
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setenv("MYKFA_LIB", str(tmp_path / "nope.so"))
+    with pytest.raises(RuntimeError, match="no fallback"):
+        _lib.lib()
