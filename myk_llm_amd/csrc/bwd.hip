@@ -228,7 +228,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
             for (int i = 0; i < 8; ++i) {
                 const float lse_i = i < 4 ? l0[i] : l1[i - 4];
                 const float del_i = i < 4 ? d0[i] : d1[i - 4];
-                float p = fast_exp2(s[8 * kb + i] * a.qk_scale - lse_i);
+                float p = fast_exp2(fmaf(s[8 * kb + i], a.qk_scale, -lse_i));
                 if (masked) {
                     const int qi = m0 + 16 * kb + 8 * g + i;
                     const int rel = key - qi;
@@ -416,7 +416,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_dq_kernel(BwdArgs a) {
             float dsv[16];
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                float p = fast_exp2(st[r] * a.qk_scale - lse_q);
+                float p = fast_exp2(fmaf(st[r], a.qk_scale, -lse_q));
                 if (masked) {
                     const int key = n0 + nb * 32 + out_row32(r, g);
                     const int rel = key - qi;

@@ -13,6 +13,8 @@ typedef short s16x8 __attribute__((ext_vector_type(8)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -21,6 +23,9 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 constexpr float kNegFloor = -1e30f;  // finite row-max floor (flash_attn.py:136-137)
+// A running softmax max is only raised when a tile exceeds it by more than this (log2 units),
+// bounding unnormalized probabilities by 2^8.
+constexpr float kRescaleSlack = 8.0f;
 
 // ---- element types -------------------------------------------------------------------
 
@@ -33,8 +38,15 @@ struct BF16 {
     __device__ static inline float to_float(uint16_t x) {
         return __uint_as_float(((uint32_t)x) << 16);
     }
+    // Two floats rounded to nearest even and packed in one v_cvt_pk_bf16_f32.
     __device__ static inline uint32_t pack2(float a, float b) {
-        return (uint32_t)from_float(a) | ((uint32_t)from_float(b) << 16);
+        bf16x2 r = {(__bf16)a, (__bf16)b};
+        return __builtin_bit_cast(uint32_t, r);
+    }
+    // c + x.lo + x.hi for a packed pair, in fp32 (v_dot2c_f32_bf16 against (1, 1)).
+    __device__ static inline float sum2(uint32_t x, float c) {
+        const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x), ones, c, false);
     }
     // C(32x32) += A(32x16) * B(16x32); lane l holds A[l%32][8(l/32)+i], B[8(l/32)+i][l%32].
     __device__ static inline f32x16 mfma32(s16x8 a, s16x8 b, f32x16 c) {
@@ -58,7 +70,12 @@ struct FP16 {
         return (float)__builtin_bit_cast(_Float16, x);
     }
     __device__ static inline uint32_t pack2(float a, float b) {
-        return (uint32_t)from_float(a) | ((uint32_t)from_float(b) << 16);
+        f16x2 r = {(_Float16)a, (_Float16)b};
+        return __builtin_bit_cast(uint32_t, r);
+    }
+    __device__ static inline float sum2(uint32_t x, float c) {
+        const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, x), ones, c, false);
     }
     __device__ static inline f32x16 mfma32(s16x8 a, s16x8 b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
@@ -105,13 +122,16 @@ __device__ inline s16x8 cat4(s16x4 a, s16x4 b) {
 
 // ---- LDS layout -----------------------------------------------------------------------
 // Tiles of ROWS x D 16-bit elements live row-major in LDS as 16-byte chunks; chunk c of row
-// r is stored at chunk position c ^ swz(r). swz spreads the rows that one MFMA operand read
-// touches together (rows {0-3, 8-11} and {4-7, 12-15} of every 16, see perm32) over
-// distinct 16-byte bank groups.
+// r is stored at chunk position c ^ swz(r), swz(r) = 2 (r mod 4) + bit 3 of r. The two
+// access patterns then touch 8 distinct 16-byte slots (128 bytes, every bank once):
+//  - a row-operand read (8 lanes, 16 bytes each): rows {0-3, 8-11} (or {4-7, 12-15}) of a
+//    16-row group at one chunk c (see perm32) -> swz takes the 8 values 0..7;
+//  - a transpose read (16 lanes, 8 bytes each): 4 consecutive rows r0..r0+3 at chunks c and
+//    c + 1 (c even) -> c ^ (2i + b) and (c + 1) ^ (2i + b), i = 0..3, are 8 distinct slots.
 template <int D>
 __device__ inline int lds_swz(int row) {
     constexpr int CPR = D / 8;  // chunks per row
-    return ((row & 3) | ((row >> 1) & 4)) & (CPR - 1);
+    return (((row & 3) << 1) | ((row >> 3) & 1)) & (CPR - 1);
 }
 template <int D>
 __device__ inline int lds_off(int row, int col) {  // element offset of (row, col)

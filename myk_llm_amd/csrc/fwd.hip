@@ -1,19 +1,21 @@
 // Prefill forward: O and base-2 LSE (replaces _fwd_kernel, flash_attn.py:106-154).
 //
-// Work decomposition. A workgroup is 4 waves; every wave owns 32 query rows of one head.
-// The workgroup's waves cover `hpw` query heads of ONE GQA group (hpw = gcd(group, 4)) times
-// 4 / hpw blocks of 32 consecutive tokens, so each K/V tile staged in LDS serves every
-// query head of the group that the workgroup holds: K/V bytes are fetched once per group.
+// Work decomposition. A workgroup is NW waves (8, or 4 for small/large head_dim); every wave
+// owns 32 query rows of one head. The workgroup's waves cover `hpw` query heads of ONE GQA
+// group (hpw = gcd(group, NW)) times NW / hpw blocks of 32 consecutive tokens, so each K/V
+// tile staged in LDS serves every query head of the group that the workgroup holds: K/V
+// bytes are fetched once per group.
 //
 // Per 64-key tile, each wave computes S^T = K Q^T on 32x32x16 bf16 MFMA (K from LDS as the
 // A operand, Q resident in registers as the B operand), so that the output lane of every
-// score is its query and the registers are keys. The online softmax (row max through a
-// permlane32 swap, exp2 on the fp32 scores) then produces P^T already in the k-operand
-// layout of the next product O^T += V^T P^T, whose A operand (V^T) is read straight from
-// the row-major V tile with the gfx950 LDS transpose read. K/V tiles are double-buffered in
-// LDS with an XOR chunk swizzle. Key tiles wholly outside a wave's causal/window band are
-// skipped, and only tiles that cross the band edge evaluate the element mask (the 3-range
-// split of flash_attn.py:140-145).
+// score is its query and the registers are keys. The online softmax (row max on raw scores
+// through a permlane32 swap, one FMA + exp2 per score, lazy rescaling of O) then produces
+// P^T already in the k-operand layout of the next product O^T += V^T P^T, whose A operand
+// (V^T) is read straight from the row-major V tile with the gfx950 LDS transpose read. K/V
+// tiles arrive through an asynchronous LDS ring (buffer_load ... lds, STAGES - 1 tiles
+// ahead) in an XOR-swizzled layout; one workgroup barrier per tile. Key tiles wholly outside
+// a wave's causal/window band are skipped, and only tiles that cross the band edge evaluate
+// the element mask (the 3-range split of flash_attn.py:140-145).
 #include "common.h"
 #include "kernels.h"
 
@@ -49,12 +51,12 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdArgs a) {
     using Ring = TileRing<D, BN, 2, NW>;  // K and V tiles
     __shared__ __attribute__((aligned(16))) uint16_t smem[STAGES][2][BN * D];
 
-    const int tid = threadIdx.x;
+    const int tid = __builtin_amdgcn_workitem_id_x();
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int l32 = lane & 31, g = lane >> 5;
     const int tpw = NW / a.hpw;
     // Logical block (query block fastest, then head group, then sequence), XCD-grouped.
-    const int logical = xcd_logical(blockIdx.x);
+    const int logical = xcd_logical(__builtin_amdgcn_workgroup_id_x());
     if (logical >= a.gx * a.gy * a.gz) return;
     const int mblk = a.gx - 1 - logical % a.gx;  // longest causal rows first (flash_attn.py:115)
     const int h_first = (logical / a.gx) % a.gz * a.hpw;
@@ -94,15 +96,19 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdArgs a) {
     const int tstride[2] = {(int)(a.kts * 2), (int)(a.vts * 2)};
 
     // Q rows of this wave as the B operand of S^T = K Q^T: lane holds Q[s0 + l32][16kk + 8g + i].
+    // A negative scale is applied as |scale| on sign-flipped Q (exact), so the row max can be
+    // taken on raw scores.
     s16x8 qop[KD];
     const int qi = s0 + l32;
+    const float c = fabsf(a.qk_scale);
     {
         const uint16_t* qp = a.q + (int64_t)b * a.qbs + (qs.tok0 + qi) * a.qts + (int64_t)h * a.qhs;
+        const short flip = a.qk_scale < 0.f ? (short)0x8000 : (short)0;
 #pragma unroll
         for (int kk = 0; kk < KD; ++kk) {
             s16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
             if (qi < q_len) v = ld16(qp + 16 * kk + 8 * g);
-            qop[kk] = v;
+            qop[kk] = v ^ flip;
         }
     }
     // Q must have landed before the ring's loads join the same in-order counter; otherwise
@@ -136,7 +142,7 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdArgs a) {
         const bool masked = !(n0 >= wr.mid_lo && n0 + BN <= wr.mid_hi);
         const uint16_t* Ks = smem[t % STAGES][0];
         const uint16_t* Vs = smem[t % STAGES][1];
-        // S^T = K Q^T, 32 keys per block.
+        // S^T = K Q^T (raw scores), 32 keys per block.
         f32x16 st[NB];
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
@@ -149,26 +155,39 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdArgs a) {
                 st[nb] = T::mfma32(kop, qop[kk], st[nb]);
             }
         }
-        // Online softmax (flash_attn.py:90-96) on scaled scores.
-        float mx = kNegFloor;
+        // Band mask, only on tiles that cross the band edge (flash_attn.py:140-145).
+        if (masked) {
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = n0 + nb * 32 + out_row32(r, g);
+                    const int rel = key - qi;
+                    if (!(rel >= lo_off && rel <= hi_off && key < k_len)) st[nb][r] = -INFINITY;
+                }
+        }
+        // Online softmax (flash_attn.py:90-96). The row max is taken on the raw scores (c > 0)
+        // and the scale is folded into one FMA per score: p = exp2(s c - m).
+        float mx = -INFINITY;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                float x = st[nb][r] * a.qk_scale;
-                if (masked) {
-                    const int key = n0 + nb * 32 + out_row32(r, g);
-                    const int rel = key - qi;
-                    const bool vis = rel >= lo_off && rel <= hi_off && key < k_len;
-                    x = vis ? x : -INFINITY;
-                }
-                st[nb][r] = x;
-                mx = fmaxf(mx, x);
-            }
-        mx = max_halves(mx);
-        const float m_new = fmaxf(m_i, mx);
-        const float alpha = fast_exp2(m_i - m_new);
-        float lsum = 0.f;
+            for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(st[nb][r], st[nb][r + 1]));
+        mx = max_halves(mx) * c;
+        // Lazy rescaling: the running max m moves only when a tile exceeds it by more than
+        // kRescaleSlack, so P stays <= 2^kRescaleSlack; O / l and the LSE use the same m, so the
+        // result is unchanged while most tiles skip the O rescale entirely.
+        if (__builtin_amdgcn_ballot_w64(mx > m_i + kRescaleSlack) != 0) {
+            const float m_new = mx > m_i + kRescaleSlack ? mx : m_i;
+            const float alpha = fast_exp2(m_i - m_new);
+            l_i *= alpha;
+            m_i = m_new;
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
+        }
+        const float neg_m = -m_i;
         s16x8 pop[KB];
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
@@ -177,20 +196,14 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdArgs a) {
                 uint32_t w[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    float p0 = fast_exp2(st[nb][8 * half + 2 * i] - m_new);
-                    float p1 = fast_exp2(st[nb][8 * half + 2 * i + 1] - m_new);
-                    lsum += p0 + p1;
+                    const float p0 = fast_exp2(fmaf(st[nb][8 * half + 2 * i], c, neg_m));
+                    const float p1 = fast_exp2(fmaf(st[nb][8 * half + 2 * i + 1], c, neg_m));
                     w[i] = T::pack2(p0, p1);
+                    l_i += p0 + p1;  // fp32 row sum (flash_attn.py:96): the LSE needs it unrounded
                 }
                 u32x4 wv = {w[0], w[1], w[2], w[3]};
                 pop[nb * 2 + half] = __builtin_bit_cast(s16x8, wv);
             }
-        l_i = l_i * alpha + lsum;
-        m_i = m_new;
-#pragma unroll
-        for (int db = 0; db < DB; ++db)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
         // O^T += V^T P^T; V^T operand through the LDS transpose read.
         const int G = lane >> 4, jj = lane & 15;
 #pragma unroll
@@ -262,7 +275,7 @@ hipError_t launch_dtype(const FwdArgs& args, int D, int batch, int num_heads, in
         case 16: return launch_typed<16, 64, 4, 4, T>(args, batch, num_heads, max_q, s);
         case 32: return launch_typed<32, 64, 4, 4, T>(args, batch, num_heads, max_q, s);
         case 64: return launch_typed<64, 64, 8, 4, T>(args, batch, num_heads, max_q, s);
-        case 128: return launch_typed<128, 64, 8, 3, T>(args, batch, num_heads, max_q, s);
+        case 128: return launch_typed<128, 64, 8, 4, T>(args, batch, num_heads, max_q, s);
         case 256: return launch_typed<256, 32, 4, 3, T>(args, batch, num_heads, max_q, s);
         default: return hipErrorInvalidValue;
     }
