@@ -42,7 +42,7 @@ struct BwdArgs {
     int hpw;
     int num_heads;
     int batch;
-    int gx, gy, gz;  // logical grid (fastest first), XCD-grouped by the launchers
+    int gx, gy, gz;  // blocks per (group, sequence), sequences, groups; decoded by block_coord
 };
 
 // ---- 1. delta = rowsum(dO * O) ---------------------------------------------------------
@@ -118,15 +118,18 @@ __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
     const int l32 = lane & 31, g = lane >> 5;
     const int hpw = a.hpw, kpw = NW / hpw;
     const int kb_w = wave / hpw, hs = wave % hpw;
-    // Logical block: key block fastest, then KV head, then sequence (XCD-grouped).
-    const int logical = xcd_logical(blockIdx.x);
-    if (logical >= a.gx * a.gy * a.gz) return;
-    const int n0 = (logical % a.gx) * 32 * kpw;  // causal: the first key blocks see the most queries
-    const int kvh = (logical / a.gx) % a.gz;
-    const int b = logical / (a.gx * a.gz);
+    // Key blocks are ranked from the END of each sequence: under a causal mask key block n of
+    // a sequence of nblk blocks sees nblk - n query blocks, so equal ranks carry equal work in
+    // every sequence and rank 0 (the first key block of the longest sequences) starts first.
+    const BlockCoord bc = block_coord(xcd_logical(blockIdx.x), a.gz, a.gy);
+    if (bc.rank >= a.gx) return;
+    const int kvh = bc.group;
+    const int b = bc.seq;
     SeqInfo ks = seq_info(b, a.cu_k, nullptr, a.seqlen_k, false);
     const int k_len = ks.len;
-    if (n0 >= k_len) return;
+    const int kblk = bc.rank - (a.gx - (k_len + 32 * kpw - 1) / (32 * kpw));
+    if (kblk < 0) return;
+    const int n0 = kblk * 32 * kpw;
     SeqInfo qs = seq_info(b, a.cu_q, nullptr, a.seqlen_q, false);
     const int q_len = qs.len;
     // Query i sees key j iff (i - j) in [q_len - k_len - wr, q_len - k_len + wl]
@@ -318,12 +321,12 @@ __global__ __launch_bounds__(NW * 64) void bwd_dq_kernel(BwdArgs a) {
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int l32 = lane & 31, g = lane >> 5;
     const int tpw = NW / a.hpw;
-    // Logical block: query block fastest (longest rows first), then head group, then sequence.
-    const int logical = xcd_logical(blockIdx.x);
-    if (logical >= a.gx * a.gy * a.gz) return;
-    const int mblk = a.gx - 1 - logical % a.gx;
-    const int h_first = (logical / a.gx) % a.gz * a.hpw;
-    const int b = logical / (a.gx * a.gz);
+    // Longest causal rows first across all heads and sequences, XCD-grouped.
+    const BlockCoord bc = block_coord(xcd_logical(blockIdx.x), a.gz, a.gy);
+    if (bc.rank >= a.gx) return;
+    const int mblk = a.gx - 1 - bc.rank;
+    const int h_first = bc.group * a.hpw;
+    const int b = bc.seq;
     SeqInfo qs = seq_info(b, a.cu_q, nullptr, a.seqlen_q, false);
     const int tok_base = mblk * tpw * 32;
     if (tok_base >= qs.len) return;
@@ -524,7 +527,7 @@ hipError_t dkdv_launch(BwdArgs a, int num_kv_heads, hipStream_t s) {
     a.gx = (a.seqlen_k + keys_per_wg - 1) / keys_per_wg;
     a.gy = a.batch;
     a.gz = num_kv_heads;
-    const long long n = (long long)a.gx * a.gy * a.gz;
+    const long long n = block_grid_size(a.gx, a.gz, a.gy);
     if (n == 0) return hipSuccess;
     if (n > (1LL << 30)) return hipErrorInvalidConfiguration;
     hipLaunchKernelGGL((bwd_dkdv_kernel<D, NW, STAGES, T>), dim3(xcd_grid((int)n)), dim3(NW * 64), 0, s, a);
@@ -550,7 +553,7 @@ hipError_t dq_launch(BwdArgs a, hipStream_t s) {
     a.gx = (a.seqlen_q + tpw * 32 - 1) / (tpw * 32);
     a.gy = a.batch;
     a.gz = a.num_heads / a.hpw;
-    const long long n = (long long)a.gx * a.gy * a.gz;
+    const long long n = block_grid_size(a.gx, a.gz, a.gy);
     if (n == 0) return hipSuccess;
     if (n > (1LL << 30)) return hipErrorInvalidConfiguration;
     hipLaunchKernelGGL((bwd_dq_kernel<D, BN, NW, STAGES, T>), dim3(xcd_grid((int)n)), dim3(NW * 64), 0, s, a);

@@ -264,6 +264,28 @@ __device__ inline int xcd_logical(int pid) {
     return ((slot / kXcdChunk) * kXcds + xcd) * kXcdChunk + slot % kXcdChunk;
 }
 
+// Block order for grids whose per-block work is skewed (causal rows or keys). A logical id
+// decodes block-rank-slowest: ranks r*kXcdChunk .. r*kXcdChunk + kXcdChunk - 1 of every
+// (group, sequence) are dispatched before the next run of ranks, so the longest blocks of ALL
+// heads and sequences start first (longest-processing-time order; a doc-major order leaves
+// the long causal blocks of the last sequences for the tail) while each run of kXcdChunk
+// consecutive blocks of one (group, sequence) still executes on one XCD. Ranks >= the block
+// count (padding) are for the caller to skip.
+struct BlockCoord {
+    int rank, group, seq;
+};
+__device__ inline BlockCoord block_coord(int logical, int groups, int seqs) {
+    const int lo = logical % kXcdChunk, rest = logical / kXcdChunk;
+    BlockCoord c;
+    c.group = rest % groups;
+    c.seq = (rest / groups) % seqs;
+    c.rank = rest / (groups * seqs) * kXcdChunk + lo;
+    return c;
+}
+inline long long block_grid_size(int nblk, int groups, int seqs) {
+    return (long long)((nblk + kXcdChunk - 1) / kXcdChunk) * kXcdChunk * groups * seqs;
+}
+
 // ---- sequences --------------------------------------------------------------------------
 
 struct SeqInfo {

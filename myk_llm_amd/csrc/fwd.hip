@@ -38,12 +38,12 @@ struct FwdArgs {
     float qk_scale;  // softmax_scale * log2(e)  (flash_attn.py:368)
     int group;       // num_heads / num_kv_heads
     int hpw;         // query heads per workgroup
-    int gx, gy, gz;  // logical grid: query blocks x sequences x head groups
+    int gx, gy, gz;  // query blocks, sequences, head groups; decoded by block_coord
 };
 
 // Stage a BN x D tile (rows n0.., masked to < len) from global into a swizzled LDS tile.
 template <int D, int BN, int NW, int STAGES, typename T>
-__global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdArgs a) {
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4 : 1))) void fwd_kernel(FwdArgs a) {
     constexpr int KD = D / 16;            // k-steps of S^T = K Q^T
     constexpr int DB = (D + 31) / 32;     // 32-row blocks of O^T
     constexpr int NB = BN / 32;           // 32-key blocks per tile
@@ -55,12 +55,13 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int l32 = lane & 31, g = lane >> 5;
     const int tpw = NW / a.hpw;
-    // Logical block (query block fastest, then head group, then sequence), XCD-grouped.
-    const int logical = xcd_logical(__builtin_amdgcn_workgroup_id_x());
-    if (logical >= a.gx * a.gy * a.gz) return;
-    const int mblk = a.gx - 1 - logical % a.gx;  // longest causal rows first (flash_attn.py:115)
-    const int h_first = (logical / a.gx) % a.gz * a.hpw;
-    const int b = logical / (a.gx * a.gz);
+    // Longest causal rows first across all heads and sequences (flash_attn.py:115 orders
+    // within one head only), XCD-grouped.
+    const BlockCoord bc = block_coord(xcd_logical(__builtin_amdgcn_workgroup_id_x()), a.gz, a.gy);
+    if (bc.rank >= a.gx) return;
+    const int mblk = a.gx - 1 - bc.rank;
+    const int h_first = bc.group * a.hpw;
+    const int b = bc.seq;
 
     SeqInfo qs = seq_info(b, a.cu_q, nullptr, a.seqlen_q, false);
     const int tok_base = mblk * tpw * 32;
@@ -261,7 +262,7 @@ hipError_t launch_typed(FwdArgs args, int batch, int num_heads, int max_q, hipSt
     args.gx = (max_q + tpw * 32 - 1) / (tpw * 32);
     args.gy = batch;
     args.gz = num_heads / args.hpw;
-    const long long n = (long long)args.gx * args.gy * args.gz;
+    const long long n = block_grid_size(args.gx, args.gz, args.gy);
     if (n == 0) return hipSuccess;
     if (n > (1LL << 30)) return hipErrorInvalidConfiguration;
     hipLaunchKernelGGL((fwd_kernel<D, BN, NW, STAGES, T>), dim3(xcd_grid((int)n)), dim3(NW * 64), 0, s, args);
