@@ -30,6 +30,9 @@ HIPFLAGS = [
     "-std=c++17",
     "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in ordinary VGPRs: the softmax reads every score with VALU instructions, and
+    # the default heuristic's AGPR destinations cost one v_accvgpr_read per score per tile.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wno-unused-command-line-argument",
 ]
 # Per-source extras. fwd.hip: scores are never NaN for finite inputs (the reference's output

@@ -165,10 +165,18 @@ __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
         for (int r = 0; r < 16; ++r) dk[db][r] = dv[db][r] = 0.f;
 
     uint16_t* ring = smem[wave][0];
-    auto issue = [&](int it) {
-        const int h = kvh * a.group + hs + hpw * (it / ntiles);
-        const int m0 = wr.lo + (it % ntiles) * BMQ;
-        uint16_t* st = ring + (it % STAGES) * STAGE;
+    // Iteration it streams query tile it % ntiles of head hs + hpw * (it / ntiles); the issue
+    // side keeps its own (tile, head) counters so the loop does no integer division.
+    int iss_tile = 0, iss_head = kvh * a.group + hs, iss_stage = 0;
+    auto issue = [&]() {
+        const int h = iss_head;
+        const int m0 = wr.lo + iss_tile * BMQ;
+        uint16_t* st = ring + iss_stage * STAGE;
+        iss_stage = iss_stage + 1 == STAGES ? 0 : iss_stage + 1;
+        if (++iss_tile == ntiles) {
+            iss_tile = 0;
+            iss_head += hpw;
+        }
         const uint16_t* qb = a.q + (int64_t)b * a.qbs + qs.tok0 * a.qts + (int64_t)h * a.qhs;
         const uint16_t* db_ = a.dout + (int64_t)b * a.dobs + qs.tok0 * a.dots + (int64_t)h * a.dohs;
         const i32x4 rq = rows_rsrc(qb, q_len, a.qts, D);
@@ -195,16 +203,19 @@ __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
     };
 #pragma unroll
     for (int t = 0; t < STAGES - 1; ++t)
-        if (t < iters) issue(t);
+        if (t < iters) issue();
 
+    int cur_tile = 0, cur_stage = 0;
     for (int it = 0; it < iters; ++it) {
         const int after = iters - 1 - it < STAGES - 2 ? iters - 1 - it : STAGES - 2;
         ring_wait<LOADS, STAGES>(after);
         wait_lgkmcnt0();  // this wave's reads of the stage about to be refilled have returned
-        if (it + STAGES - 1 < iters) issue(it + STAGES - 1);
-        const int m0 = wr.lo + (it % ntiles) * BMQ;
+        if (it + STAGES - 1 < iters) issue();
+        const int m0 = wr.lo + cur_tile * BMQ;
         const bool masked = !(m0 >= wr.mid_lo && m0 + BMQ <= wr.mid_hi);
-        const uint16_t* st = ring + (it % STAGES) * STAGE;
+        const uint16_t* st = ring + cur_stage * STAGE;
+        cur_tile = cur_tile + 1 == ntiles ? 0 : cur_tile + 1;
+        cur_stage = cur_stage + 1 == STAGES ? 0 : cur_stage + 1;
         const uint16_t* Qs = st;
         const uint16_t* DOs = st + TILE;
         const float* fl = reinterpret_cast<const float*>(st + 2 * TILE);
@@ -218,30 +229,42 @@ __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
             dp = T::mfma32(lds_row_op<D>(DOs, 0, l32, g, kk), vop[kk], dp);
         }
         const int key = nw0 + l32;
-        s16x8 pb[2], dsb[2];
+        // Register r = 8 kb + i holds query row m0 + 16 kb + 8 g + i; its lse / delta sit at
+        // floats [16 kb + 8 g + i] / [32 + 16 kb + 8 g + i] of the stage.
+        float pv[16], lsev[16], delv[16];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
-            // Rows 16 kb + 8 g + i, i = 0..7 (registers 8 kb + i).
             const f32x4 l0 = *reinterpret_cast<const f32x4*>(fl + 16 * kb + 8 * g);
             const f32x4 l1 = *reinterpret_cast<const f32x4*>(fl + 16 * kb + 8 * g + 4);
             const f32x4 d0 = *reinterpret_cast<const f32x4*>(fl + 32 + 16 * kb + 8 * g);
             const f32x4 d1 = *reinterpret_cast<const f32x4*>(fl + 32 + 16 * kb + 8 * g + 4);
-            float pv[8], dsv[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float lse_i = i < 4 ? l0[i] : l1[i - 4];
-                const float del_i = i < 4 ? d0[i] : d1[i - 4];
-                float p = fast_exp2(fmaf(s[8 * kb + i], a.qk_scale, -lse_i));
-                if (masked) {
-                    const int qi = m0 + 16 * kb + 8 * g + i;
-                    const int rel = key - qi;
-                    p = (rel >= lo_f && rel <= hi_f && qi < q_len && key < k_len) ? p : 0.f;
-                }
-                pv[i] = p;
-                dsv[i] = p * (dp[8 * kb + i] - del_i);
+            for (int i = 0; i < 4; ++i) {
+                lsev[8 * kb + i] = l0[i];
+                lsev[8 * kb + 4 + i] = l1[i];
+                delv[8 * kb + i] = d0[i];
+                delv[8 * kb + 4 + i] = d1[i];
             }
-            u32x4 pw = {T::pack2(pv[0], pv[1]), T::pack2(pv[2], pv[3]), T::pack2(pv[4], pv[5]),
-                        T::pack2(pv[6], pv[7])};
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) pv[r] = fast_exp2(fmaf(s[r], a.qk_scale, -lsev[r]));
+        // Band mask, only on tiles that cross the band edge (flash_attn.py:294-296).
+        if (masked) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int qi = m0 + 16 * (r >> 3) + 8 * g + (r & 7);
+                const int rel = key - qi;
+                pv[r] = (rel >= lo_f && rel <= hi_f && qi < q_len && key < k_len) ? pv[r] : 0.f;
+            }
+        }
+        s16x8 pb[2], dsb[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            float dsv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) dsv[i] = pv[8 * kb + i] * (dp[8 * kb + i] - delv[8 * kb + i]);
+            const float* pk = pv + 8 * kb;
+            u32x4 pw = {T::pack2(pk[0], pk[1]), T::pack2(pk[2], pk[3]), T::pack2(pk[4], pk[5]), T::pack2(pk[6], pk[7])};
             u32x4 dw = {T::pack2(dsv[0], dsv[1]), T::pack2(dsv[2], dsv[3]), T::pack2(dsv[4], dsv[5]),
                         T::pack2(dsv[6], dsv[7])};
             pb[kb] = __builtin_bit_cast(s16x8, pw);
