@@ -158,6 +158,14 @@ __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
         }
     }
     wait_vmcnt<0>();  // K/V landed before the ring's loads share the counter
+    // Output rows of this lane's key, formed here so that no kernel argument stays live
+    // across the main loop (they would be spilled from scalar registers).
+    const int out_key = nw0 + l32;
+    uint16_t* const dkp = a.dk + (int64_t)b * a.dkbs + (ks.tok0 + out_key) * a.dkts + (int64_t)kvh * a.dkhs;
+    uint16_t* const dvp = a.dv + (int64_t)b * a.dvbs + (ks.tok0 + out_key) * a.dvts + (int64_t)kvh * a.dvhs;
+    const float sm_scale = a.sm_scale, qk_scale = sgpr_copy(a.qk_scale);
+    const int64_t q_hstep = (int64_t)hpw * a.qhs, do_hstep = (int64_t)hpw * a.dohs;
+    const int64_t f_hstep = (int64_t)hpw * a.lse_hs, qts = sgpr_copy(a.qts), dots = sgpr_copy(a.dots);
     f32x16 dk[DB], dv[DB];
 #pragma unroll
     for (int db = 0; db < DB; ++db)
@@ -165,41 +173,52 @@ __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
         for (int r = 0; r < 16; ++r) dk[db][r] = dv[db][r] = 0.f;
 
     uint16_t* ring = smem[wave][0];
-    // Iteration it streams query tile it % ntiles of head hs + hpw * (it / ntiles); the issue
-    // side keeps its own (tile, head) counters so the loop does no integer division.
-    int iss_tile = 0, iss_head = kvh * a.group + hs, iss_stage = 0;
+    const uint32_t ring_lds = lds_addr(ring);
+    // Iteration it streams query tile it % ntiles of head hs + hpw * (it / ntiles). The issue
+    // side keeps its own (tile, head) state: stream pointers of its current head, advanced by
+    // hpw heads after ntiles tiles, so the loop does no division and little 64-bit math.
+    const int h0 = kvh * a.group + hs;
+    const uint16_t* iq = a.q + (int64_t)b * a.qbs + qs.tok0 * a.qts + (int64_t)h0 * a.qhs;
+    const uint16_t* ido = a.dout + (int64_t)b * a.dobs + qs.tok0 * a.dots + (int64_t)h0 * a.dohs;
+    const float* ilse = a.lse + (int64_t)h0 * a.lse_hs + qs.row0;
+    const float* idel = a.delta + (int64_t)h0 * a.lse_hs + qs.row0;  // lse's (head, row) layout
+    // Lane offsets inside a 32-row tile (row-relative, swizzled 16-byte chunk): the tile's
+    // first row goes into the buffer base, so these are loop-invariant.
+    unsigned q_lane[QLOADS], do_lane[QLOADS];
+#pragma unroll
+    for (int j = 0; j < QLOADS; ++j) {
+        const int p = j * 64 + lane;
+        const int row = p / CPR, logical = (p % CPR) ^ lds_swz<D>(row);
+        q_lane[j] = (unsigned)(row * (int)(a.qts * 2) + logical * 16);
+        do_lane[j] = (unsigned)(row * (int)(a.dots * 2) + logical * 16);
+    }
+    const unsigned f_lane = (unsigned)((lane & 31) * 4);
+    int iss_tile = 0, iss_stage = 0;
     auto issue = [&]() {
-        const int h = iss_head;
         const int m0 = wr.lo + iss_tile * BMQ;
-        uint16_t* st = ring + iss_stage * STAGE;
-        iss_stage = iss_stage + 1 == STAGES ? 0 : iss_stage + 1;
-        if (++iss_tile == ntiles) {
-            iss_tile = 0;
-            iss_head += hpw;
-        }
-        const uint16_t* qb = a.q + (int64_t)b * a.qbs + qs.tok0 * a.qts + (int64_t)h * a.qhs;
-        const uint16_t* db_ = a.dout + (int64_t)b * a.dobs + qs.tok0 * a.dots + (int64_t)h * a.dohs;
-        const i32x4 rq = rows_rsrc(qb, q_len, a.qts, D);
-        const i32x4 rd = rows_rsrc(db_, q_len, a.dots, D);
+        const uint32_t st = ring_lds + iss_stage * (STAGE * 2);
+        // Rows m0.. of the current head; rows at or beyond q_len read 0.
+        const i32x4 rq = rows_rsrc(iq + m0 * qts, q_len - m0, qts, D);
+        const i32x4 rd = rows_rsrc(ido + m0 * dots, q_len - m0, dots, D);
 #pragma unroll
         for (int j = 0; j < QLOADS; ++j) {
-            const int p = j * 64 + lane;
-            const int row = p / CPR, phys = p % CPR;
-            const int logical = phys ^ lds_swz<D>(row);
-            const unsigned oq = (unsigned)((m0 + row) * (int)(a.qts * 2) + logical * 16);
-            const unsigned od = (unsigned)((m0 + row) * (int)(a.dots * 2) + logical * 16);
-            dma16(rq, lds_addr(st + j * 512), oq);
-            dma16(rd, lds_addr(st + TILE + j * 512), od);
+            dma16(rq, st + j * 1024, q_lane[j]);
+            dma16(rd, st + (TILE + j * 512) * 2, do_lane[j]);
         }
         // lse into floats [0, 32), delta into [32, 64) of the stage's float area; rows at or
         // beyond q_len read 0 (their probabilities are masked to 0).
-        const float* lb = a.lse + (int64_t)h * a.lse_hs + qs.row0;
-        const float* dl = a.delta + (int64_t)h * a.lse_hs + qs.row0;
-        const int64_t fbytes = (int64_t)q_len * 4;
-        const i32x4 rl = buffer_rsrc(lb, fbytes), rdl = buffer_rsrc(dl, fbytes);
-        const uint32_t fl = lds_addr(st + 2 * TILE);
-        if (lane < 32) dma4(rl, fl, (unsigned)((m0 + lane) * 4));
-        if (lane >= 32) dma4(rdl, fl, (unsigned)((m0 + lane - 32) * 4));
+        const int64_t fbytes = (int64_t)(q_len - m0) * 4;
+        const uint32_t fl = st + 2 * TILE * 2;
+        if (lane < 32) dma4(buffer_rsrc(ilse + m0, fbytes), fl, f_lane);
+        if (lane >= 32) dma4(buffer_rsrc(idel + m0, fbytes), fl, f_lane);
+        iss_stage = iss_stage + 1 == STAGES ? 0 : iss_stage + 1;
+        if (++iss_tile == ntiles) {
+            iss_tile = 0;
+            iq += q_hstep;
+            ido += do_hstep;
+            ilse += f_hstep;
+            idel += f_hstep;
+        }
     };
 #pragma unroll
     for (int t = 0; t < STAGES - 1; ++t)
@@ -247,7 +266,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
             }
         }
 #pragma unroll
-        for (int r = 0; r < 16; ++r) pv[r] = fast_exp2(fmaf(s[r], a.qk_scale, -lsev[r]));
+        for (int r = 0; r < 16; ++r) pv[r] = fast_exp2(fmaf(s[r], qk_scale, -lsev[r]));
         // Band mask, only on tiles that cross the band edge (flash_attn.py:294-296).
         if (masked) {
 #pragma unroll
@@ -309,18 +328,15 @@ __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
     }
 
     // Store dK * sm_scale and dV (flash_attn.py:312-314); lane column = key, rows = d.
-    const int key = nw0 + l32;
-    if (hs == 0 && bs > 0 && key < k_len) {
-        uint16_t* dkp = a.dk + (int64_t)b * a.dkbs + (ks.tok0 + key) * a.dkts + (int64_t)kvh * a.dkhs;
-        uint16_t* dvp = a.dv + (int64_t)b * a.dvbs + (ks.tok0 + key) * a.dvts + (int64_t)kvh * a.dvhs;
+    if (hs == 0 && bs > 0 && out_key < k_len) {
 #pragma unroll
         for (int db = 0; db < DB; ++db)
 #pragma unroll
             for (int rq = 0; rq < 4; ++rq) {
                 const int d0 = 32 * db + 8 * rq + 4 * g;
                 if (d0 < D) {
-                    u32x2 wk = {T::pack2(dk[db][4 * rq] * a.sm_scale, dk[db][4 * rq + 1] * a.sm_scale),
-                                T::pack2(dk[db][4 * rq + 2] * a.sm_scale, dk[db][4 * rq + 3] * a.sm_scale)};
+                    u32x2 wk = {T::pack2(dk[db][4 * rq] * sm_scale, dk[db][4 * rq + 1] * sm_scale),
+                                T::pack2(dk[db][4 * rq + 2] * sm_scale, dk[db][4 * rq + 3] * sm_scale)};
                     u32x2 wv = {T::pack2(dv[db][4 * rq], dv[db][4 * rq + 1]),
                                 T::pack2(dv[db][4 * rq + 2], dv[db][4 * rq + 3])};
                     *reinterpret_cast<u32x2*>(dkp + d0) = wk;

@@ -17,6 +17,7 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
@@ -40,8 +41,10 @@ struct BF16 {
     }
     // Two floats rounded to nearest even and packed in one v_cvt_pk_bf16_f32.
     __device__ static inline uint32_t pack2(float a, float b) {
-        bf16x2 r = {(__bf16)a, (__bf16)b};
-        return __builtin_bit_cast(uint32_t, r);
+        // A 2-vector conversion: two scalar casts compile to two half-empty conversions and a
+        // v_perm_b32 to merge them.
+        const f32x2 v = {a, b};
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
     }
     // c + x.lo + x.hi for a packed pair, in fp32 (v_dot2c_f32_bf16 against (1, 1)).
     __device__ static inline float sum2(uint32_t x, float c) {
@@ -70,8 +73,8 @@ struct FP16 {
         return (float)__builtin_bit_cast(_Float16, x);
     }
     __device__ static inline uint32_t pack2(float a, float b) {
-        f16x2 r = {(_Float16)a, (_Float16)b};
-        return __builtin_bit_cast(uint32_t, r);
+        const f32x2 v = {a, b};
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
     }
     __device__ static inline float sum2(uint32_t x, float c) {
         const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
@@ -102,6 +105,21 @@ __device__ inline float max_halves(float x) {
 __device__ inline float sum_halves(float x) {
     auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// A fresh scalar copy of a wave-uniform value. Kernel arguments arrive as wide scalar-load
+// tuples; a loop that keeps one element live keeps (and, under pressure, spills) the whole
+// tuple, while an opaque copy lets the tuple die.
+__device__ inline int sgpr_copy(int x) {
+    x = __builtin_amdgcn_readfirstlane(x);
+    asm volatile("" : "+s"(x));
+    return x;
+}
+__device__ inline float sgpr_copy(float x) { return __int_as_float(sgpr_copy(__float_as_int(x))); }
+__device__ inline int64_t sgpr_copy(int64_t x) {
+    const uint32_t lo = (uint32_t)sgpr_copy((int)(uint32_t)x);
+    const uint32_t hi = (uint32_t)sgpr_copy((int)(uint32_t)((uint64_t)x >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
 // 16-byte and 8-byte global accesses.
