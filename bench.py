@@ -119,6 +119,31 @@ class KernelCalls:
         _lib.check(self.L.mykfa_bwd_dq(ctypes.byref(self.bp), self.stream))
 
 
+class DecodeCalls:
+    """Prepared C-ABI calls of the split-K decode and its merge on one cache set."""
+
+    def __init__(self, q, kc, vc, lens, scale):
+        self.L = _lib.lib()
+        b, nq, h, d = q.shape
+        self.out = torch.empty_like(q)
+        self.lse = torch.empty((h, b * nq), dtype=torch.float32, device=q.device)
+        wl, wr = fa._window(True, (-1, -1))
+        fp = fa._fwd_params(q, kc, vc, self.out, self.lse, None, None, lens, nq, kc.shape[1], scale, wl, wr)
+        self.dp = _lib.DecodeParams()
+        self.dp.fwd = fp
+        self.dp.num_splits = self.L.mykfa_decode_num_splits(b, kc.shape[2], kc.shape[1])
+        n = self.L.mykfa_decode_workspace_size(b, h, nq, d, self.dp.num_splits)
+        self.ws = torch.empty(max(n, 16), dtype=torch.uint8, device=q.device)
+        self.keep = [q, kc, vc, lens]
+        self.stream = torch.cuda.current_stream().cuda_stream
+
+    def splitk(self):
+        _lib.check(self.L.mykfa_decode_splitk(ctypes.byref(self.dp), self.ws.data_ptr(), self.ws.numel(), self.stream))
+
+    def merge(self):
+        _lib.check(self.L.mykfa_decode_merge(ctypes.byref(self.dp), self.ws.data_ptr(), self.ws.numel(), self.stream))
+
+
 # --- workloads ----------------------------------------------------------------------------------
 
 
@@ -204,8 +229,23 @@ def measure_decode(w, steps: int, warmup: int):
         it[0] += 1
 
     ms = time_events(replay, steps * nsets, warmup=nsets)
-    del sets, graphs
-    return ms
+    # Per-kernel durations through the C ABI, alternating the cache sets as above (the lengths
+    # already include the appended tokens).
+    scale = 1.0 / (w.head_dim ** 0.5)
+    calls = [DecodeCalls(q, kc, vc, lens, scale) for kc, vc in sets]
+    it2 = [0]
+
+    def one(name):
+        def f():
+            getattr(calls[it2[0] % nsets], name)()
+            it2[0] += 1
+        return f
+
+    kern = {"decode_splitk": time_events(one("splitk"), steps * nsets, warmup=nsets),
+            "decode_merge": time_events(one("merge"), steps * nsets, warmup=nsets)}
+    splits = calls[0].dp.num_splits
+    del sets, graphs, calls
+    return ms, kern, splits
 
 
 # --- CPU baseline ---------------------------------------------------------------------------------
@@ -303,11 +343,12 @@ def main():
         for name in ("cfg5", "cfg5_mtp"):
             wk = W[name]
             log(f"config {wk.name} decode")
-            m = measure_decode(wk, max(10, args.steps // 2), 3)
+            m, kk, splits = measure_decode(wk, max(10, args.steps // 2), 3)
             gbs = wk.decode_bytes / (m * 1e-3) / 1e9
             configs[name] = {"workload": wk.name, "ms": round(m, 5), "GB/s": round(gbs, 1),
-                             "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "bytes": int(wk.decode_bytes)}
-            log(f"  {m * 1e3:.1f} us, {gbs:.0f} GB/s")
+                             "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "bytes": int(wk.decode_bytes),
+                             "splits": splits, "kernel_ms": {k: round(v, 5) for k, v in kk.items()}}
+            log(f"  {m * 1e3:.1f} us, {gbs:.0f} GB/s; kernels (ms): " + ", ".join(f"{k}={v:.4f}" for k, v in kk.items()))
     cpu = None
     if not (args.quick or args.no_cpu):
         log("cpu baseline")

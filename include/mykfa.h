@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define MYKFA_ABI_VERSION 1
+#define MYKFA_ABI_VERSION 2
 #define MYKFA_UNBOUNDED (1 << 30) /* flash_attn.py:32 (_UNBOUNDED) */
 
 /* Status codes. */
@@ -106,14 +106,25 @@ typedef struct mykfa_bwd_params {
 /*
  * KV-cache decode parameters (flash_attn_with_kvcache, flash_attn.py:467-490, run as a
  * split-K forward). q (batch, seqlen_q, H, D); caches (batch, capacity, Hkv, D) with a
- * contiguous last dimension; the keys of sequence b are cache rows [0, seqused_k[b]),
- * clamped to [0, capacity] (all capacity rows when seqused_k is NULL).
+ * contiguous last dimension; the keys of sequence b are cache rows
+ * [0, seqused_k[b] + seqlen_new), clamped to [0, capacity] (all capacity rows when seqused_k
+ * is NULL, which requires seqlen_new = 0).
+ * New keys of this step (flash_attn_with_kvcache's k, v; flash_attn.py:480-485): with k_new
+ * and v_new non-NULL the decode itself first writes them into the caches at rows
+ * seqused_k[b] + t, t < seqlen_new (rows at or beyond the capacity are dropped), so fwd.k and
+ * fwd.v are written through; with both NULL the seqlen_new rows must already be there
+ * (mykfa_kv_append).
  * Partial results of each split go to a caller-provided workspace
  * (mykfa_decode_workspace_size) and are combined by an LSE merge.
  */
 typedef struct mykfa_decode_params {
     mykfa_fwd_params fwd;   /* cu_seqlens_* must be NULL; seqused_k NULL = max_seqlen_k keys */
     int32_t num_splits;     /* 0 = choose (mykfa_decode_num_splits) */
+    int32_t seqlen_new;     /* new keys per sequence after seqused_k[b] (0 = none) */
+    const void* k_new;      /* (batch, seqlen_new, Hkv, D) or NULL */
+    const void* v_new;
+    int64_t kn_batch_stride, kn_token_stride, kn_head_stride;
+    int64_t vn_batch_stride, vn_token_stride, vn_head_stride;
 } mykfa_decode_params;
 
 /* KV append: cache[b, cache_seqlens[b] + t] = new[b, t] for t < seqlen_new
@@ -182,7 +193,8 @@ int mykfa_decode_splitk(const mykfa_decode_params* p, void* workspace, size_t wo
 /* LSE merge of the per-split partials into o and lse. */
 int mykfa_decode_merge(const mykfa_decode_params* p, const void* workspace,
                        size_t workspace_bytes, mykfa_stream_t stream);
-/* split-K + merge (replaces _forward's decode configuration, flash_attn.py:364, :488). */
+/* split-K + merge (replaces _forward's decode configuration, flash_attn.py:364, :488, and,
+ * with k_new / v_new, the cache writes of flash_attn_with_kvcache, flash_attn.py:480-485). */
 int mykfa_decode(const mykfa_decode_params* p, void* workspace, size_t workspace_bytes,
                  mykfa_stream_t stream);
 

@@ -12,6 +12,7 @@ import os
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmykfa.so"
+ABI_VERSION = 2  # MYKFA_ABI_VERSION
 
 OK = 0
 ERR_INVALID = 1
@@ -54,7 +55,11 @@ class BwdParams(ctypes.Structure):
 
 
 class DecodeParams(ctypes.Structure):
-    _fields_ = [("fwd", FwdParams), ("num_splits", _i32)]
+    _fields_ = [
+        ("fwd", FwdParams), ("num_splits", _i32), ("seqlen_new", _i32), ("k_new", _ptr), ("v_new", _ptr),
+        ("kn_batch_stride", _i64), ("kn_token_stride", _i64), ("kn_head_stride", _i64),
+        ("vn_batch_stride", _i64), ("vn_token_stride", _i64), ("vn_head_stride", _i64),
+    ]
 
 
 class KvAppendParams(ctypes.Structure):
@@ -128,8 +133,8 @@ def lib() -> ctypes.CDLL:
         fn = getattr(handle, name)
         fn.restype = restype
         fn.argtypes = argtypes
-    if handle.mykfa_abi_version() != 1:
-        raise RuntimeError(f"{path}: ABI version {handle.mykfa_abi_version()} != 1")
+    if handle.mykfa_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"{path}: ABI version {handle.mykfa_abi_version()} != {ABI_VERSION}")
     for name, struct in _STRUCT_SIZES.items():
         size = getattr(handle, name)()
         if size != ctypes.sizeof(struct):

@@ -39,7 +39,10 @@ bool head_dim_supported(int d) { return d == 16 || d == 32 || d == 64 || d == 12
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 bool stride_ok(int64_t s) { return s >= 0 && (s & 7) == 0; }
 
-int check_tensor(const void* ptr, int64_t bs, int64_t ts, int64_t hs, const char* name, bool needed) {
+// The kernels address the rows of one (sequence, head) through a buffer descriptor with a
+// 32-bit byte range: rows * token stride must stay within 2 GiB.
+int check_tensor(const void* ptr, int64_t bs, int64_t ts, int64_t hs, const char* name, bool needed,
+                 int64_t rows, int head_dim) {
     if (!needed) return MYKFA_OK;
     if (ptr == nullptr) return fail(MYKFA_ERR_INVALID, "%s is NULL", name);
     if (!aligned16(ptr)) return fail(MYKFA_ERR_INVALID, "%s must be 16-byte aligned", name);
@@ -47,6 +50,10 @@ int check_tensor(const void* ptr, int64_t bs, int64_t ts, int64_t hs, const char
         return fail(MYKFA_ERR_INVALID,
                     "%s strides (%lld, %lld, %lld) must be non-negative multiples of 8 elements", name,
                     (long long)bs, (long long)ts, (long long)hs);
+    if (ts > (1LL << 24)) return fail(MYKFA_ERR_UNSUPPORTED, "%s token stride %lld exceeds 2^24", name, (long long)ts);
+    if (rows > 0 && ((rows - 1) * ts + head_dim) * 2 > 0x7fffffffLL)
+        return fail(MYKFA_ERR_UNSUPPORTED, "%s: %lld rows at token stride %lld span more than 2 GiB", name,
+                    (long long)rows, (long long)ts);
     return MYKFA_OK;
 }
 
@@ -81,11 +88,11 @@ int check_fwd(const mykfa_fwd_params* p) {
         return fail(MYKFA_ERR_INVALID, "packed (varlen) tensors must have batch stride 0");
     const bool work = p->batch > 0 && p->max_seqlen_q > 0;
     int rc;
-    if ((rc = check_tensor(p->q, p->q_batch_stride, p->q_token_stride, p->q_head_stride, "q", work))) return rc;
-    if ((rc = check_tensor(p->o, p->o_batch_stride, p->o_token_stride, p->o_head_stride, "o", work))) return rc;
+    if ((rc = check_tensor(p->q, p->q_batch_stride, p->q_token_stride, p->q_head_stride, "q", work, p->max_seqlen_q, p->head_dim))) return rc;
+    if ((rc = check_tensor(p->o, p->o_batch_stride, p->o_token_stride, p->o_head_stride, "o", work, p->max_seqlen_q, p->head_dim))) return rc;
     const bool keys = work && p->max_seqlen_k > 0;
-    if ((rc = check_tensor(p->k, p->k_batch_stride, p->k_token_stride, p->k_head_stride, "k", keys))) return rc;
-    if ((rc = check_tensor(p->v, p->v_batch_stride, p->v_token_stride, p->v_head_stride, "v", keys))) return rc;
+    if ((rc = check_tensor(p->k, p->k_batch_stride, p->k_token_stride, p->k_head_stride, "k", keys, p->max_seqlen_k, p->head_dim))) return rc;
+    if ((rc = check_tensor(p->v, p->v_batch_stride, p->v_token_stride, p->v_head_stride, "v", keys, p->max_seqlen_k, p->head_dim))) return rc;
     if (work && p->lse == nullptr) return fail(MYKFA_ERR_INVALID, "lse is NULL");
     if (work && p->lse_head_stride < (varlen_q ? 0 : (int64_t)p->batch * p->max_seqlen_q))
         return fail(MYKFA_ERR_INVALID, "lse_head_stride %lld is smaller than the number of rows",
@@ -100,10 +107,10 @@ int check_bwd(const mykfa_bwd_params* p) {
     if (p->fwd.seqused_k != nullptr) return fail(MYKFA_ERR_INVALID, "the backward pass takes no seqused_k");
     const bool work = p->fwd.batch > 0 && p->fwd.max_seqlen_q > 0;
     const bool keys = p->fwd.batch > 0 && p->fwd.max_seqlen_k > 0;
-    if ((rc = check_tensor(p->dout, p->do_batch_stride, p->do_token_stride, p->do_head_stride, "dout", work))) return rc;
-    if ((rc = check_tensor(p->dq, p->dq_batch_stride, p->dq_token_stride, p->dq_head_stride, "dq", work))) return rc;
-    if ((rc = check_tensor(p->dk, p->dk_batch_stride, p->dk_token_stride, p->dk_head_stride, "dk", keys))) return rc;
-    if ((rc = check_tensor(p->dv, p->dv_batch_stride, p->dv_token_stride, p->dv_head_stride, "dv", keys))) return rc;
+    if ((rc = check_tensor(p->dout, p->do_batch_stride, p->do_token_stride, p->do_head_stride, "dout", work, p->fwd.max_seqlen_q, p->fwd.head_dim))) return rc;
+    if ((rc = check_tensor(p->dq, p->dq_batch_stride, p->dq_token_stride, p->dq_head_stride, "dq", work, p->fwd.max_seqlen_q, p->fwd.head_dim))) return rc;
+    if ((rc = check_tensor(p->dk, p->dk_batch_stride, p->dk_token_stride, p->dk_head_stride, "dk", keys, p->fwd.max_seqlen_k, p->fwd.head_dim))) return rc;
+    if ((rc = check_tensor(p->dv, p->dv_batch_stride, p->dv_token_stride, p->dv_head_stride, "dv", keys, p->fwd.max_seqlen_k, p->fwd.head_dim))) return rc;
     if (work && p->delta == nullptr) return fail(MYKFA_ERR_INVALID, "delta is NULL");
     if (p->fwd.cu_seqlens_q != nullptr &&
         (p->do_batch_stride != 0 || p->dq_batch_stride != 0 || p->dk_batch_stride != 0 || p->dv_batch_stride != 0))
@@ -118,6 +125,20 @@ int check_decode(const mykfa_decode_params* p) {
     if (p->fwd.cu_seqlens_q != nullptr) return fail(MYKFA_ERR_INVALID, "decode takes the dense layout only");
     if (p->num_splits < 0 || p->num_splits > 1024)
         return fail(MYKFA_ERR_INVALID, "num_splits must lie in [0, 1024]; got %d", p->num_splits);
+    if (p->seqlen_new < 0) return fail(MYKFA_ERR_INVALID, "seqlen_new must be >= 0; got %d", p->seqlen_new);
+    if (p->seqlen_new > 0 && p->fwd.seqused_k == nullptr)
+        return fail(MYKFA_ERR_INVALID, "seqlen_new > 0 needs seqused_k (the cached lengths)");
+    if ((p->k_new == nullptr) != (p->v_new == nullptr))
+        return fail(MYKFA_ERR_INVALID, "k_new and v_new must both be given or both be NULL");
+    const bool append = p->k_new != nullptr && p->seqlen_new > 0 && p->fwd.batch > 0;
+    if ((rc = check_tensor(p->k_new, p->kn_batch_stride, p->kn_token_stride, p->kn_head_stride, "k_new", append,
+                           p->seqlen_new, p->fwd.head_dim)))
+        return rc;
+    if ((rc = check_tensor(p->v_new, p->vn_batch_stride, p->vn_token_stride, p->vn_head_stride, "v_new", append,
+                           p->seqlen_new, p->fwd.head_dim)))
+        return rc;
+    if (append && (p->fwd.k == nullptr || p->fwd.v == nullptr))
+        return fail(MYKFA_ERR_INVALID, "appending new keys needs the caches k and v");
     return ok();
 }
 
@@ -133,10 +154,10 @@ int check_append(const mykfa_kv_append_params* p) {
     const bool work = p->batch > 0 && p->seqlen_new > 0;
     if (work && p->cache_seqlens == nullptr) return fail(MYKFA_ERR_INVALID, "cache_seqlens is NULL");
     int rc;
-    if ((rc = check_tensor(p->k_cache, p->kc_batch_stride, p->kc_token_stride, p->kc_head_stride, "k_cache", work))) return rc;
-    if ((rc = check_tensor(p->v_cache, p->vc_batch_stride, p->vc_token_stride, p->vc_head_stride, "v_cache", work))) return rc;
-    if ((rc = check_tensor(p->k_new, p->kn_batch_stride, p->kn_token_stride, p->kn_head_stride, "k", work))) return rc;
-    if ((rc = check_tensor(p->v_new, p->vn_batch_stride, p->vn_token_stride, p->vn_head_stride, "v", work))) return rc;
+    if ((rc = check_tensor(p->k_cache, p->kc_batch_stride, p->kc_token_stride, p->kc_head_stride, "k_cache", work, p->capacity, p->head_dim))) return rc;
+    if ((rc = check_tensor(p->v_cache, p->vc_batch_stride, p->vc_token_stride, p->vc_head_stride, "v_cache", work, p->capacity, p->head_dim))) return rc;
+    if ((rc = check_tensor(p->k_new, p->kn_batch_stride, p->kn_token_stride, p->kn_head_stride, "k", work, p->seqlen_new, p->head_dim))) return rc;
+    if ((rc = check_tensor(p->v_new, p->vn_batch_stride, p->vn_token_stride, p->vn_head_stride, "v", work, p->seqlen_new, p->head_dim))) return rc;
     return ok();
 }
 

@@ -7,14 +7,16 @@
 // is read from HBM once per GQA group, not once per query head. With GROUP = 4 and the
 // 4-query MTP draft this exactly fills the tile.
 //
-// Split-K. Workgroup (split, batch, kv-head-and-row-tile) covers the keys
-// [split * chunk, (split + 1) * chunk) of its sequence; its 4 waves take interleaved 32-key
-// tiles. Per tile a wave computes S^T = K Q^T (16x16x32 MFMA, K loaded from HBM straight
-// into A-operand registers, one tile ahead), runs the online softmax, and accumulates
-// O^T += V^T P^T with V staged in wave-private LDS and read back transposed. The waves
-// merge through LDS; a workgroup then writes either the final O/LSE (one split) or an fp32
-// partial (O, lse) that the merge kernel combines: lse = log2(sum_s 2^lse_s),
-// O = sum_s 2^(lse_s - lse) O_s.
+// Split-K. Workgroup (split, batch, unit block) covers the keys [split * chunk, (split + 1) *
+// chunk) of its sequence for kWaves consecutive (KV head, row tile) units, one per wave, so the
+// waves of a workgroup read adjacent heads of the same cache rows (contiguous DRAM rows in the
+// usual (batch, token, head, d) layout) and share nothing: no barrier, no cross-wave merge.
+// A wave streams its keys in 32-key tiles through a ring of NBUF register tiles filled by
+// bounds-checked buffer loads (NBUF - 1 tiles in flight while one computes): S^T = K Q^T on
+// 16x16x32 MFMA with K straight from the registers, the online softmax, and O^T += V^T P^T
+// with V staged in wave-private, double-buffered LDS and read back transposed. A wave then
+// writes either the final O/LSE (one split) or an fp32 partial (O, lse) that the merge kernel
+// combines: lse = log2(sum_s 2^lse_s), O = sum_s 2^(lse_s - lse) O_s.
 #include "common.h"
 #include "kernels.h"
 
@@ -41,18 +43,24 @@ struct DecodeArgs {
     int group;
     int rows;      // group * nq
     int row_tiles; // ceil(rows / 16)
+    int units;     // num_kv_heads * row_tiles (one wave each)
     int num_heads;
     int chunk;     // keys per split (multiple of kTile)
     int splits;
-    float* ws_o;   // [splits][batch][num_heads][nq][D]
-    float* ws_lse; // [splits][batch][num_heads][nq]
+    int n_new;     // keys appended after seqused_k[b] in this step
+    const uint16_t* kn;  // new keys / values to write into the caches first, or null
+    const uint16_t* vn;
+    int64_t knbs, knts, knhs, vnbs, vnts, vnhs;
+    float* ws_o;   // [batch][num_heads][nq][splits][D]: a row's partials are contiguous
+    float* ws_lse; // [batch][num_heads][nq][splits]
     int batch;
 };
 
-// Keys of sequence b, clamped to the cache capacity so no read leaves the cache.
+// Keys of sequence b (cached plus this step's new ones), clamped to the cache capacity so
+// no read leaves the cache.
 __device__ inline int seq_keys(const DecodeArgs& a, int b) {
     if (!a.seqused_k) return a.cap;
-    const int L = a.seqused_k[b];
+    const int L = a.seqused_k[b] + a.n_new;
     return L < 0 ? 0 : (L > a.cap ? a.cap : L);
 }
 
@@ -63,27 +71,56 @@ __device__ inline Ranges decode_ranges(const DecodeArgs& a, int L) {
     return block_ranges(0, a.nq, lo_off, hi_off, L, kTile);
 }
 
+// Register ring depth (32-key tiles of K and V in flight per wave) by head_dim: one tile
+// holds 2 * 32 * D bytes in 32 * D / 64 * 2 / 4 VGPRs.
+template <int D>
+constexpr int decode_nbuf() { return D <= 64 ? 4 : 2; }
+
 template <int D, typename T>
 __global__ __launch_bounds__(kThreads) void decode_splitk_kernel(DecodeArgs a) {
     constexpr int KD = D < 32 ? 1 : D / 32;  // 32-wide d steps of S^T (D = 16 pads to 32)
     constexpr int DB = (D + 15) / 16;        // 16-row blocks of O^T
-    constexpr int VPL = (kTile * D / 8 + 63) / 64;  // 16-byte V chunks per lane per tile
-    __shared__ __attribute__((aligned(16))) uint16_t vlds[kWaves][kTile * D];
-    __shared__ float red_m[kWaves][16], red_l[kWaves][16];
-    __shared__ float red_o[kWaves][16][D + 1];
+    constexpr int VPL = kTile * D / 8 / 64 > 0 ? kTile * D / 8 / 64 : 1;  // V chunks per lane
+    constexpr int NBUF = decode_nbuf<D>();
+    static_assert(kTile * D / 8 >= 64 && (kTile * D / 8) % 64 == 0, "V tile is whole 64-lane loads");
+    __shared__ __attribute__((aligned(16))) uint16_t vlds[kWaves][2][kTile * D];
 
-    const int split = blockIdx.x, b = blockIdx.y;
-    const int kvh = blockIdx.z / a.row_tiles, rt = blockIdx.z % a.row_tiles;
-    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int tid = __builtin_amdgcn_workitem_id_x();
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int l16 = lane & 15, G = lane >> 4;
+    const int split = blockIdx.x, b = blockIdx.y;
+    // Wave = one (KV head, row tile) unit; the waves of a workgroup take consecutive units,
+    // i.e. adjacent heads of the same cache rows. No state is shared between waves.
+    const int unit = blockIdx.z * kWaves + wave;
+    if (unit >= a.units) return;
+    const int kvh = unit / a.row_tiles, rt = unit % a.row_tiles;
 
     const int L = seq_keys(a, b);
+    if (a.kn) {
+        // This step's new keys first (flash_attn.py:480-485): the wave writes the rows of its KV
+        // head that fall in its split's key range, whatever their visibility, and drops rows at
+        // or beyond the capacity. Every wave reading a row wrote it itself (waves of further row
+        // tiles of a head write identical copies), and the wait below orders its stores before
+        // its loads.
+        const int base = a.seqused_k[b];
+        constexpr int CPR = D / 8;
+        for (int i = lane; i < a.n_new * CPR; i += 64) {
+            const int t = i / CPR, ch = i % CPR;
+            const int pos = base + t;
+            if (pos < 0 || pos >= a.cap || pos / a.chunk != split) continue;
+            const int64_t src_k = (int64_t)b * a.knbs + (int64_t)t * a.knts + (int64_t)kvh * a.knhs + ch * 8;
+            const int64_t src_v = (int64_t)b * a.vnbs + (int64_t)t * a.vnts + (int64_t)kvh * a.vnhs + ch * 8;
+            const int64_t dst_k = (int64_t)b * a.kbs + (int64_t)pos * a.kts + (int64_t)kvh * a.khs + ch * 8;
+            const int64_t dst_v = (int64_t)b * a.vbs + (int64_t)pos * a.vts + (int64_t)kvh * a.vhs + ch * 8;
+            st16(const_cast<uint16_t*>(a.k) + dst_k, ld16(a.kn + src_k));
+            st16(const_cast<uint16_t*>(a.v) + dst_v, ld16(a.vn + src_v));
+        }
+    }
     const Ranges rg = decode_ranges(a, L);
     int k0 = split * a.chunk, k1 = k0 + a.chunk;
     k0 = k0 > rg.lo ? k0 : rg.lo;
     k1 = k1 < rg.hi ? k1 : rg.hi;
     if (a.splits > 1 && k0 >= k1) return;  // this split holds no visible key: the merge skips it
-
     const int lo_off = band_lo(L, a.nq, a.wl), hi_off = band_hi(L, a.nq, a.wr);
 
     // Q^T operand: lane holds Q[row l16][32 kk + 8 G + i].
@@ -102,52 +139,78 @@ __global__ __launch_bounds__(kThreads) void decode_splitk_kernel(DecodeArgs a) {
             qop[kk] = v;
         }
     }
+    // Q landed (and any appended rows stored) before the ring's loads share the in-order
+    // counter; otherwise the counter analysis cannot bound the loop's pending loads and drains
+    // them at the loop head.
+    wait_vmcnt<0>();
 
+    // K / V rows 0 .. L-1 of this (sequence, KV head) through bounds-checked buffer loads: keys
+    // at or beyond L read 0 and a load whose offset is at or above 2^31 fetches nothing, which
+    // is how tiles past the split's end are skipped without a branch.
     const uint16_t* kbase = a.k + (int64_t)b * a.kbs + (int64_t)kvh * a.khs;
     const uint16_t* vbase = a.v + (int64_t)b * a.vbs + (int64_t)kvh * a.vhs;
-    uint16_t* vs = vlds[wave];
+    const int64_t kspan = L > 0 ? ((int64_t)(L - 1) * a.kts + D) * 2 : 0;
+    const int64_t vspan = L > 0 ? ((int64_t)(L - 1) * a.vts + D) * 2 : 0;
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(kbase), (short)0, (int)(kspan < 0x7fffffff ? kspan : 0x7fffffff), 0x00020000);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(vbase), (short)0, (int)(vspan < 0x7fffffff ? vspan : 0x7fffffff), 0x00020000);
+    const unsigned kts2 = (unsigned)(a.kts * 2), vts2 = (unsigned)(a.vts * 2);
+    // Tile offset of a tile past the split's end: every lane offset plus it lies in
+    // [2^31, 2^32), outside any buffer (lane offsets stay below 2^31: 31 token strides at most).
+    constexpr unsigned kSkip = 0x80000000u;
+    // Loop-invariant lane offsets inside a tile. K block kb holds keys 8 (rho / 4) + 4 kb +
+    // rho % 4 in its 16 rows (the order of the score registers).
+    unsigned koff[2][KD], voff[VPL];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int kk = 0; kk < KD; ++kk) {
+            const int key = 8 * (l16 >> 2) + 4 * kb + (l16 & 3);
+            const int d0 = 32 * kk + 8 * G;
+            koff[kb][kk] = (unsigned)key * kts2 + (d0 < D ? d0 : 0) * 2;
+        }
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        const int idx = lane + 64 * i;
+        voff[i] = (unsigned)(idx / (D / 8)) * vts2 + (idx % (D / 8)) * 16;
+    }
 
     f32x4 acc[DB];
 #pragma unroll
     for (int db = 0; db < DB; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m_i = kNegFloor, l_i = 0.f;
 
-    // One tile of registers: K in A-operand order (two 16-key blocks), V as row chunks.
     struct TileRegs {
         s16x8 k[2][KD];
         s16x8 v[VPL];
     };
     auto load_tile = [&](int t0, TileRegs& tr) {
+        const unsigned kt = t0 < k1 ? (unsigned)t0 * kts2 : kSkip;
+        const unsigned vt = t0 < k1 ? (unsigned)t0 * vts2 : kSkip;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            // Block kb of the tile holds keys t0 + 8 (rho / 4) + 4 kb + rho % 4 in its rows.
-            const int key = t0 + 8 * (l16 >> 2) + 4 * kb + (l16 & 3);
+        for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
             for (int kk = 0; kk < KD; ++kk) {
-                s16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
-                const int d0 = 32 * kk + 8 * G;
-                if (key < L && d0 < D) v = ld16(kbase + (int64_t)key * a.kts + d0);
+                s16x8 v = __builtin_bit_cast(s16x8, __builtin_amdgcn_raw_buffer_load_b128(krs, koff[kb][kk] + kt, 0, 0));
+                if (32 * kk + 8 * G >= D) v = s16x8{0, 0, 0, 0, 0, 0, 0, 0};  // D = 16 pads d to 32
                 tr.k[kb][kk] = v;
             }
-        }
+#pragma unroll
+        for (int i = 0; i < VPL; ++i)
+            tr.v[i] = __builtin_bit_cast(s16x8, __builtin_amdgcn_raw_buffer_load_b128(vrs, voff[i] + vt, 0, 0));
+        // Keep tiles in issue order: the in-order load counter can then wait for the oldest
+        // tile alone; a scheduler that interleaves two tiles' loads forces a full drain.
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto compute_tile = [&](int t0, const TileRegs& tr, int parity) {
+        // Stage V in this wave's LDS (swizzled, double-buffered) for the transpose read.
+        uint16_t* vs = vlds[wave][parity];
 #pragma unroll
         for (int i = 0; i < VPL; ++i) {
             const int idx = lane + 64 * i;
             const int r = idx / (D / 8), ch = idx % (D / 8);
-            s16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
-            if (idx < kTile * D / 8 && t0 + r < L) v = ld16(vbase + (int64_t)(t0 + r) * a.vts + ch * 8);
-            tr.v[i] = v;
-        }
-    };
-    auto compute_tile = [&](int t0, const TileRegs& tr) {
-        // Stage this tile's V rows in wave-private LDS (swizzled) for the transpose read.
-#pragma unroll
-        for (int i = 0; i < VPL; ++i) {
-            const int idx = lane + 64 * i;
-            if (idx < kTile * D / 8) {
-                const int r = idx / (D / 8), ch = idx % (D / 8);
-                *reinterpret_cast<s16x8*>(vs + r * D + ((ch ^ lds_swz<D>(r)) << 3)) = tr.v[i];
-            }
+            *reinterpret_cast<s16x8*>(vs + r * D + ((ch ^ lds_swz<D>(r)) << 3)) = tr.v[i];
         }
         // S^T = K Q^T for the two 16-key blocks of the tile.
         f32x4 st[2];
@@ -157,24 +220,27 @@ __global__ __launch_bounds__(kThreads) void decode_splitk_kernel(DecodeArgs a) {
 #pragma unroll
             for (int kk = 0; kk < KD; ++kk) st[kb] = T::mfma16(tr.k[kb][kk], qop[kk], st[kb]);
         }
-        const bool masked = !(t0 >= rg.mid_lo && t0 + kTile <= rg.mid_hi);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) st[kb] *= a.qk_scale;
+        // Band mask, only on tiles that cross the band edge or the end of the cache.
+        if (!(t0 >= rg.mid_lo && t0 + kTile <= rg.mid_hi)) {
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int key = t0 + 8 * G + 4 * kb + r;
+                    const int rel = key - qi;
+                    st[kb][r] = (rel >= lo_off && rel <= hi_off && key < L) ? st[kb][r] : -INFINITY;
+                }
+        }
         float mx = kNegFloor;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                float x = st[kb][r] * a.qk_scale;
-                if (masked) {
-                    const int key = t0 + 8 * G + 4 * kb + r;
-                    const int rel = key - qi;
-                    x = (rel >= lo_off && rel <= hi_off && key < L) ? x : -INFINITY;
-                }
-                st[kb][r] = x;
-                mx = fmaxf(mx, x);
-            }
+            for (int r = 0; r < 4; ++r) mx = fmaxf(mx, st[kb][r]);
         // Row max across the 4 lane groups holding this row (lanes l16 + 16 G).
         mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        mx = max_halves(mx);
         const float m_new = fmaxf(m_i, mx);
         const float alpha = fast_exp2(m_i - m_new);
         float p[8];
@@ -202,73 +268,59 @@ __global__ __launch_bounds__(kThreads) void decode_splitk_kernel(DecodeArgs a) {
         }
     };
 
-    // Two register tiles in flight: the next tile's loads overlap this tile's math.
-    const int step = kWaves * kTile;
-    TileRegs ta, tb;
-    int t0 = k0 + wave * kTile;
-    if (t0 < k1) load_tile(t0, ta);
-    for (; t0 < k1; t0 += 2 * step) {
-        const int t1 = t0 + step;
-        if (t1 < k1) load_tile(t1, tb);
-        compute_tile(t0, ta);
-        if (t1 >= k1) break;
-        if (t1 + step < k1) load_tile(t1 + step, ta);
-        compute_tile(t1, tb);
+    // NBUF tiles in registers: tile j computes while tiles j + 1 .. j + NBUF - 1 are in flight.
+    const int nt = k1 > k0 ? (k1 - k0 + kTile - 1) / kTile : 0;
+    TileRegs buf[NBUF];
+#pragma unroll
+    for (int i = 0; i < NBUF - 1; ++i) load_tile(k0 + i * kTile, buf[i]);
+    for (int t = 0; t < nt; t += NBUF) {
+#pragma unroll
+        for (int i = 0; i < NBUF; ++i) {
+            load_tile(k0 + (t + i + NBUF - 1) * kTile, buf[(i + NBUF - 1) % NBUF]);
+            if (t + i < nt) compute_tile(k0 + (t + i) * kTile, buf[i], i & 1);
+        }
     }
 
-    // Merge the 4 waves: row stats per lane group are partial sums over that group's keys.
-    float l_row = l_i;
-    l_row += __shfl_xor(l_row, 16);
-    l_row += __shfl_xor(l_row, 32);
-    if (G == 0) {
-        red_m[wave][l16] = m_i;
-        red_l[wave][l16] = l_row;
-    }
+    // Row sum over the 4 lane groups (each summed its own keys); the max is already common.
+    float l_row = l_i + __shfl_xor(l_i, 16);
+    l_row = sum_halves(l_row);
+    if (!row_ok) return;
+    const bool empty = l_row == 0.f;
+    const float inv = empty ? 0.f : 1.f / l_row;
+    if (a.splits == 1) {
+        // Final output (flash_attn.py:147-154): lane writes d = 16 db + 4 G .. + 3 of its row.
+        uint16_t* op = a.o + (int64_t)b * a.obs + (int64_t)qi * a.ots + (int64_t)h * a.ohs;
 #pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int d = 16 * db + 4 * G + r;
-            if (d < D) red_o[wave][l16][d] = acc[db][r];
+        for (int db = 0; db < DB; ++db) {
+            const int d0 = 16 * db + 4 * G;
+            if (d0 < D) {
+                u32x2 w = {T::pack2(acc[db][0] * inv, acc[db][1] * inv), T::pack2(acc[db][2] * inv, acc[db][3] * inv)};
+                *reinterpret_cast<u32x2*>(op + d0) = w;
+            }
         }
-    __syncthreads();
-    // Each thread finalizes (row, d) pairs of the tile.
-    for (int idx = tid; idx < 16 * D; idx += kThreads) {
-        const int rr = idx / D, d = idx % D;
-        const int grow = rt * 16 + rr;
-        if (grow >= a.rows) continue;
-        float M = kNegFloor;
+        if (G == 0) a.lse[(int64_t)h * a.lse_hs + (int64_t)b * a.nq + qi] = empty ? INFINITY : m_i + fast_log2(l_row);
+    } else {
+        // Normalized partial: O_s = o / l, lse_s = m + log2(l) (-inf when empty).
+        const int64_t prow = ((((int64_t)b * a.num_heads + h) * a.nq + qi) * a.splits) + split;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, red_m[w][rr]);
-        float lt = 0.f, ot = 0.f;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-            const float s = fast_exp2(red_m[w][rr] - M);
-            lt += red_l[w][rr] * s;
-            ot += red_o[w][rr][d] * s;
+        for (int db = 0; db < DB; ++db) {
+            const int d0 = 16 * db + 4 * G;
+            if (d0 < D) *reinterpret_cast<f32x4*>(a.ws_o + prow * D + d0) = acc[db] * inv;
         }
-        const int hh = kvh * a.group + grow / a.nq, qq = grow % a.nq;
-        if (a.splits == 1) {
-            // Final output (flash_attn.py:147-154).
-            const bool empty = lt == 0.f;
-            const float val = empty ? 0.f : ot / lt;
-            a.o[(int64_t)b * a.obs + (int64_t)qq * a.ots + (int64_t)hh * a.ohs + d] = T::from_float(val);
-            if (d == 0)
-                a.lse[(int64_t)hh * a.lse_hs + (int64_t)b * a.nq + qq] = empty ? INFINITY : M + fast_log2(lt);
-        } else {
-            // Normalized partial: O_s = ot / lt, lse_s = M + log2(lt) (-inf when empty).
-            const int64_t prow = (((int64_t)split * a.batch + b) * a.num_heads + hh) * a.nq + qq;
-            const bool empty = lt == 0.f;
-            a.ws_o[prow * D + d] = empty ? 0.f : ot / lt;
-            if (d == 0) a.ws_lse[prow] = empty ? -INFINITY : M + fast_log2(lt);
-        }
+        if (G == 0) a.ws_lse[prow] = empty ? -INFINITY : m_i + fast_log2(l_row);
     }
 }
 
-// One wave per output row (batch, head, query): combines the splits that hold visible keys.
+// One wave per output row (batch, head, query): combines the splits that hold visible keys,
+// lse = log2(sum_s 2^lse_s), O = sum_s 2^(lse_s - lse) O_s. Every split's lse is loaded at once
+// (lane = split) and reduced across the wave; the partial O rows are then read as float4,
+// LPS lanes per split row and 64 / LPS split rows per load, four loads in flight per lane.
 template <int D, typename T>
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    constexpr int LPS = D / 4;       // lanes per split row (float4 each)
+    constexpr int SPI = 64 / LPS;    // split rows per wave-wide load
+    constexpr int UNROLL = 4;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int64_t rowid = (int64_t)blockIdx.x * 4 + wave;  // over batch * num_heads * nq
     const int64_t total = (int64_t)a.batch * a.num_heads * a.nq;
     if (rowid >= total) return;
@@ -277,37 +329,61 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
     const int b = rowid / ((int64_t)a.nq * a.num_heads);
     const int L = seq_keys(a, b);
     const Ranges rg = decode_ranges(a, L);
-    int s_lo = rg.lo / a.chunk, s_hi = rg.hi > rg.lo ? (rg.hi - 1) / a.chunk + 1 : s_lo;
+    const int s_lo = rg.lo / a.chunk;
+    int s_hi = rg.hi > rg.lo ? (rg.hi - 1) / a.chunk + 1 : s_lo;
     if (s_hi > a.splits) s_hi = a.splits;
-    const int64_t rstride = (int64_t)a.batch * a.num_heads * a.nq;
-    const int64_t base = ((int64_t)b * a.num_heads + hh) * a.nq + qq;
+    const int n = s_hi - s_lo;
+    const float* lse_row = a.ws_lse + rowid * a.splits + s_lo;
+    const float* o_row = a.ws_o + (rowid * a.splits + s_lo) * D;
+
+    // Max over the splits' lse (empty splits hold -inf).
     float M = -INFINITY;
-    for (int s = s_lo; s < s_hi; ++s) M = fmaxf(M, a.ws_lse[s * rstride + base]);
-    constexpr int PER = (D + 63) / 64;
-    float o[PER];
+    for (int s0 = 0; s0 < n; s0 += 64) {
+        const float v = s0 + lane < n ? lse_row[s0 + lane] : -INFINITY;
+        M = fmaxf(M, v);
+    }
 #pragma unroll
-    for (int i = 0; i < PER; ++i) o[i] = 0.f;
+    for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
+
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     float lsum = 0.f;
     if (M != -INFINITY) {
-        for (int s = s_lo; s < s_hi; ++s) {
-            const float ls = a.ws_lse[s * rstride + base];
-            const float w = fast_exp2(ls - M);  // 0 for empty splits (ls = -inf)
-            lsum += w;
-            const float* op = a.ws_o + (s * rstride + base) * D;
+        const int sub = lane / LPS, d0 = (lane % LPS) * 4;
+        for (int s0 = 0; s0 < n; s0 += 64) {
+            // Weights of splits s0 .. s0 + 63, one per lane.
+            const float w_lane = s0 + lane < n ? fast_exp2(lse_row[s0 + lane] - M) : 0.f;
+            lsum += w_lane;
+            const int cnt = n - s0 < 64 ? n - s0 : 64;
+            for (int j = 0; j < cnt; j += SPI * UNROLL) {
+                f32x4 ov[UNROLL];
+                float wv[UNROLL];
 #pragma unroll
-            for (int i = 0; i < PER; ++i) {
-                const int d = lane + 64 * i;
-                if (d < D) o[i] += w * op[d];
+                for (int u = 0; u < UNROLL; ++u) {
+                    const int sl = j + u * SPI + sub;  // split within this chunk of 64
+                    const bool ok = sl < cnt;
+                    wv[u] = __shfl(w_lane, ok ? sl : 0);
+                    ov[u] = ok ? *reinterpret_cast<const f32x4*>(o_row + (int64_t)(s0 + sl) * D + d0)
+                               : f32x4{0.f, 0.f, 0.f, 0.f};
+                    if (!ok) wv[u] = 0.f;
+                }
+#pragma unroll
+                for (int u = 0; u < UNROLL; ++u) acc += wv[u] * ov[u];
             }
         }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) lsum += __shfl_xor(lsum, off);
+        // Sum the SPI split groups (lanes d-aligned LPS apart).
+#pragma unroll
+        for (int off = LPS; off < 64; off <<= 1)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[c] += __shfl_xor(acc[c], off);
     }
     const bool empty = M == -INFINITY;
     const float inv = empty ? 0.f : 1.f / lsum;
-    uint16_t* out = a.o + (int64_t)b * a.obs + (int64_t)qq * a.ots + (int64_t)hh * a.ohs;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        const int d = lane + 64 * i;
-        if (d < D) out[d] = T::from_float(o[i] * inv);
+    if (lane < LPS) {
+        uint16_t* out = a.o + (int64_t)b * a.obs + (int64_t)qq * a.ots + (int64_t)hh * a.ohs + lane * 4;
+        u32x2 w = {T::pack2(acc[0] * inv, acc[1] * inv), T::pack2(acc[2] * inv, acc[3] * inv)};
+        *reinterpret_cast<u32x2*>(out) = w;
     }
     if (lane == 0) a.lse[(int64_t)hh * a.lse_hs + (int64_t)b * a.nq + qq] = empty ? INFINITY : M + fast_log2(lsum);
 }
@@ -315,6 +391,12 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
 DecodeArgs make_args(const mykfa_decode_params& p, int splits, void* ws) {
     const mykfa_fwd_params& f = p.fwd;
     DecodeArgs a;
+    a.n_new = p.seqlen_new;
+    const bool append = p.k_new != nullptr && p.seqlen_new > 0;
+    a.kn = append ? static_cast<const uint16_t*>(p.k_new) : nullptr;
+    a.vn = append ? static_cast<const uint16_t*>(p.v_new) : nullptr;
+    a.knbs = p.kn_batch_stride; a.knts = p.kn_token_stride; a.knhs = p.kn_head_stride;
+    a.vnbs = p.vn_batch_stride; a.vnts = p.vn_token_stride; a.vnhs = p.vn_head_stride;
     a.q = static_cast<const uint16_t*>(f.q);
     a.k = static_cast<const uint16_t*>(f.k);
     a.v = static_cast<const uint16_t*>(f.v);
@@ -334,11 +416,16 @@ DecodeArgs make_args(const mykfa_decode_params& p, int splits, void* ws) {
     a.group = f.num_heads / f.num_kv_heads;
     a.rows = a.group * a.nq;
     a.row_tiles = (a.rows + 15) / 16;
+    a.units = f.num_kv_heads * a.row_tiles;
     a.num_heads = f.num_heads;
     a.splits = splits;
     int chunk = (f.max_seqlen_k + splits - 1) / splits;
     chunk = (chunk + kTile - 1) / kTile * kTile;
-    a.chunk = chunk > 0 ? chunk : kTile;
+    chunk = chunk > 0 ? chunk : kTile;
+    // Splits start chunk cache rows apart; power-of-two distances put the concurrently
+    // starting workgroups on the same DRAM channels (measured ~15% slower), so step off them.
+    if (chunk > kTile && (chunk & (chunk - 1)) == 0) chunk += kTile;
+    a.chunk = chunk;
     a.batch = f.batch;
     const size_t rows_total = (size_t)f.batch * f.num_heads * f.max_seqlen_q;
     a.ws_o = static_cast<float*>(ws);
@@ -348,7 +435,7 @@ DecodeArgs make_args(const mykfa_decode_params& p, int splits, void* ws) {
 
 template <typename T>
 hipError_t splitk_dtype(const DecodeArgs& a, int D, int num_kv_heads, hipStream_t s) {
-    dim3 grid(a.splits, a.batch, num_kv_heads * a.row_tiles);
+    dim3 grid(a.splits, a.batch, (a.units + kWaves - 1) / kWaves);
     switch (D) {
         case 16: hipLaunchKernelGGL((decode_splitk_kernel<16, T>), grid, dim3(kThreads), 0, s, a); break;
         case 32: hipLaunchKernelGGL((decode_splitk_kernel<32, T>), grid, dim3(kThreads), 0, s, a); break;
@@ -411,13 +498,16 @@ size_t decode_workspace_bytes(int batch, int num_heads, int seqlen_q, int head_d
 }
 
 int decode_default_splits(int batch, int num_kv_heads, int capacity) {
-    // Aim for about 16 workgroups per CU on the 256-CU chip if every cache were full, with at
-    // least 256 keys per split; caches are usually partly filled, so this keeps several
-    // workgroups per CU in flight for typical fills.
-    const long long target = 256LL * 16;
-    const long long pairs = (long long)(batch > 0 ? batch : 1) * (num_kv_heads > 0 ? num_kv_heads : 1);
-    long long splits = (target + pairs - 1) / pairs;
-    const long long max_by_len = (capacity + 255) / 256;
+    // About 352 keys per split (measured best on full 16K caches: long enough to stream, short
+    // enough to balance), raised so that full caches give at least ~2048 workgroups (each
+    // kWaves KV heads of one sequence) on the 256-CU chip, and capped at 128 keys per split.
+    const long long heads = num_kv_heads > 0 ? num_kv_heads : 1;
+    const long long pairs = (long long)(batch > 0 ? batch : 1) * ((heads + kWaves - 1) / kWaves);
+    const long long cap = capacity > 0 ? capacity : 1;
+    long long splits = (cap + 351) / 352;
+    const long long fill = (2048 + pairs - 1) / pairs;
+    if (splits < fill) splits = fill;
+    const long long max_by_len = (cap + 127) / 128;
     if (splits > max_by_len) splits = max_by_len;
     if (splits > 1024) splits = 1024;
     if (splits < 1) splits = 1;

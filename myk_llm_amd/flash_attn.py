@@ -166,16 +166,36 @@ def _forward(q: Tensor, k: Tensor, v: Tensor, cu_seqlens_q: Optional[Tensor], cu
     return out, lse
 
 
-def _decode_launch(L, p: _lib.FwdParams, device: torch.device) -> None:
-    """Split-K decode with its LSE merge; the workspace comes from torch's allocator."""
+def _decode_launch(L, p: _lib.FwdParams, device: torch.device, k_new: Optional[Tensor] = None,
+                   v_new: Optional[Tensor] = None) -> None:
+    """Split-K decode with its LSE merge; the workspace comes from torch's allocator. With
+    k_new / v_new the decode first writes them into the caches after seqused_k[b]."""
     d = _lib.DecodeParams()
     d.fwd = p
-    d.num_splits = 0
     splits = L.mykfa_decode_num_splits(p.batch, p.num_kv_heads, p.max_seqlen_k)
     d.num_splits = splits
+    if k_new is not None:
+        d.seqlen_new = k_new.shape[1]
+        d.k_new, d.v_new = k_new.data_ptr(), v_new.data_ptr()
+        d.kn_batch_stride, d.kn_token_stride, d.kn_head_stride = _strides(k_new)
+        d.vn_batch_stride, d.vn_token_stride, d.vn_head_stride = _strides(v_new)
     nbytes = L.mykfa_decode_workspace_size(p.batch, p.num_heads, p.max_seqlen_q, p.head_dim, splits)
     ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=device)
     _lib.check(L.mykfa_decode(ctypes.byref(d), ws.data_ptr(), ws.numel(), _stream(device)))
+
+
+def _decode_append(q: Tensor, k_cache: Tensor, v_cache: Tensor, k: Tensor, v: Tensor, cache_seqlens: Tensor,
+                   softmax_scale: float, window_left: int, window_right: int) -> tuple[Tensor, Tensor]:
+    """flash_attn_with_kvcache for decode-sized q in one split-K launch plus its merge: the
+    decode writes k / v into the caches itself (flash_attn.py:480-488)."""
+    k, v = _kernel_ready(k), _kernel_ready(v)
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    lse = torch.empty((q.shape[-2], q.shape[0] * q.shape[1]), dtype=torch.float32, device=q.device)
+    p = _fwd_params(q, k_cache, v_cache, out, lse, None, None, cache_seqlens, q.shape[1], k_cache.shape[1],
+                    softmax_scale, window_left, window_right)
+    with _DeviceGuard(q.device):
+        _decode_launch(_lib.lib(), p, q.device, k, v)
+    return out, lse
 
 
 def _backward(dout: Tensor, q: Tensor, k: Tensor, v: Tensor, out: Tensor, lse: Tensor,
@@ -347,13 +367,25 @@ def flash_attn_with_kvcache(
         raise ValueError("the caches need a contiguous last dimension")
     q = _last_dim_contiguous(q)
     seqused = cache_seqlens.to(torch.int32)
+    scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(q.shape[-1])
+    if k is not None and v is not None:
+        # The reference's index writes (flash_attn.py:480-485) raise on a shape that does not
+        # match (batch, new, kv_heads, head_dim) of the caches; so does this.
+        want = (q.shape[0], k.shape[1], k_cache.shape[2], k_cache.shape[3])
+        if tuple(k.shape) != want or tuple(v.shape) != want:
+            raise RuntimeError(f"new keys/values of shapes {tuple(k.shape)}, {tuple(v.shape)} do not match "
+                               f"the caches: expected {want}")
+    if (k is not None and v is not None and not _compiling() and 0 < q.shape[1] <= _DECODE_MAX_Q
+            and _kernel_ready(q) is q and _kernel_ready(k_cache) is k_cache and _kernel_ready(v_cache) is v_cache):
+        _check_meta(q, k, v)
+        out, lse = _decode_append(q, k_cache, v_cache, k, v, _int32(seqused), scale, *_window(causal, window_size))
+        return (out, lse) if return_softmax_lse else out
     if k is not None and v is not None:
         if _compiling():
             _kv_append_op(k_cache, v_cache, k, v, seqused)
         else:
             _kv_append(k_cache, v_cache, k, v, seqused)
         seqused = seqused + k.shape[1]
-    scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(q.shape[-1])
     out, lse = _fwd(q, k_cache, v_cache, None, None, seqused, q.shape[1], k_cache.shape[1], scale,
                     *_window(causal, window_size))
     return (out, lse) if return_softmax_lse else out

@@ -128,3 +128,63 @@ def test_graph_capture_replays_match_eager():
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"replay {i}"
     assert torch.equal(kc_g, kc_e)
+
+
+def _decode_abi(q, kc, vc, cl, splits, kn=None, vn=None, n_new=0):
+    """mykfa_decode through the C ABI; kn / vn (or n_new pre-appended rows) are this step's keys."""
+    out = torch.empty_like(q)
+    lse = torch.empty((q.shape[2], q.shape[0] * q.shape[1]), dtype=torch.float32, device="cuda")
+    p = _lib.DecodeParams()
+    p.fwd = fa._fwd_params(q, kc, vc, out, lse, None, None, cl, q.shape[1], kc.shape[1], 0.125, _lib.UNBOUNDED, 0)
+    p.num_splits = splits
+    p.seqlen_new = kn.shape[1] if kn is not None else n_new
+    if kn is not None:
+        p.k_new, p.v_new = kn.data_ptr(), vn.data_ptr()
+        p.kn_batch_stride, p.kn_token_stride, p.kn_head_stride = fa._strides(kn)
+        p.vn_batch_stride, p.vn_token_stride, p.vn_head_stride = fa._strides(vn)
+    L = _lib.lib()
+    nbytes = L.mykfa_decode_workspace_size(p.fwd.batch, p.fwd.num_heads, p.fwd.max_seqlen_q, q.shape[-1], splits)
+    ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device="cuda")
+    _lib.check(L.mykfa_decode(ctypes.byref(p), ws.data_ptr(), ws.numel(), torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    return out, lse
+
+
+@pytest.mark.parametrize("splits", [1, 3, 7, 16])
+def test_decode_appends_new_keys_itself(splits):
+    """k_new / v_new in the decode params: the split-K kernel writes them into the caches
+    (flash_attn.py:480-485) before attending. New rows straddle split boundaries (7 splits of
+    608 keys over 4096 rows: 606..609, 1214..1217) and the capacity (4093..4096: row 4096 is
+    dropped); caches must equal the reference's bit for bit and outputs match the oracle."""
+    _say(f"fused append splits={splits}")
+    lens = [606, 1214, 0, 4093, 2000]
+    q, kc, vc, kn, vn, cl = _make(len(lens), 4096, lens, 4, 16, 4, 64, seed=5)
+    exp, exp_lse, ekc, evc = kvcache_reference(q.float(), kc.float(), vc.float(), kn.float(), vn.float(), cl, True,
+                                               (-1, -1))
+    kcg, vcg = kc.cuda(), vc.cuda()
+    out, lse = _decode_abi(q.cuda(), kcg, vcg, cl.cuda(), splits, kn.cuda(), vn.cuda())
+    assert torch.equal(kcg.cpu().float(), ekc) and torch.equal(vcg.cpu().float(), evc)
+    assert_close(out, exp)
+    assert_lse(lse, exp_lse)
+
+
+def test_decode_counts_preappended_keys():
+    """seqlen_new without k_new / v_new: the rows are already in the caches (mykfa_kv_append)
+    and the decode attends over seqused_k[b] + seqlen_new keys."""
+    lens = [10, 700, 1500]
+    q, kc, vc, kn, vn, cl = _make(len(lens), 2048, lens, 2, 8, 2, 64, seed=6)
+    exp, exp_lse, ekc, evc = kvcache_reference(q.float(), kc.float(), vc.float(), kn.float(), vn.float(), cl, True,
+                                               (-1, -1))
+    out, lse = _decode_abi(q.cuda(), ekc.to(torch.bfloat16).cuda(), evc.to(torch.bfloat16).cuda(), cl.cuda(), 5,
+                           n_new=kn.shape[1])
+    assert_close(out, exp)
+    assert_lse(lse, exp_lse)
+
+
+def test_new_keys_of_the_wrong_shape_raise():
+    q, kc, vc, kn, vn, cl = _make(2, 64, [3, 5], 1, 4, 2, 64)
+    q, kc, vc, cl = q.cuda(), kc.cuda(), vc.cuda(), cl.cuda()
+    with pytest.raises(RuntimeError):
+        flash_attn_with_kvcache(q, kc, vc, kn[:, :, :1].cuda(), vn[:, :, :1].cuda(), cache_seqlens=cl, causal=True)
+    with pytest.raises(RuntimeError):
+        flash_attn_with_kvcache(q, kc, vc, kn.cuda(), vn[:, :, :1].cuda(), cache_seqlens=cl, causal=True)
