@@ -255,14 +255,22 @@ struct TileRing {
 // Wait until the tile issued `ahead` tiles before the newest one has landed (this wave's part).
 template <int LOADS, int STAGES>
 __device__ inline void ring_wait(int tiles_after) {
-    // tiles_after = tiles issued after the awaited one, 0 .. STAGES - 2.
-    if (STAGES >= 4 && tiles_after >= 2) {
-        wait_vmcnt<(STAGES >= 4 ? 2 * LOADS : 0)>();
-    } else if (STAGES >= 3 && tiles_after >= 1) {
-        wait_vmcnt<(STAGES >= 3 ? LOADS : 0)>();
-    } else {
-        wait_vmcnt<0>();
+    // tiles_after = tiles issued after the awaited one, 0 .. STAGES - 2 (the load counter
+    // holds at most 63 outstanding loads).
+    static_assert((STAGES - 2) * LOADS <= 63, "ring deeper than the load counter");
+    if constexpr (STAGES >= 6) {
+        if (tiles_after >= 4) return wait_vmcnt<4 * LOADS>();
     }
+    if constexpr (STAGES >= 5) {
+        if (tiles_after >= 3) return wait_vmcnt<3 * LOADS>();
+    }
+    if constexpr (STAGES >= 4) {
+        if (tiles_after >= 2) return wait_vmcnt<2 * LOADS>();
+    }
+    if constexpr (STAGES >= 3) {
+        if (tiles_after >= 1) return wait_vmcnt<LOADS>();
+    }
+    wait_vmcnt<0>();
 }
 
 // ---- XCD-aware workgroup order ------------------------------------------------------------

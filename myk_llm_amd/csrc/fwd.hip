@@ -43,7 +43,7 @@ struct FwdArgs {
 
 // Stage a BN x D tile (rows n0.., masked to < len) from global into a swizzled LDS tile.
 template <int D, int BN, int NW, int STAGES, typename T>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4 : 1))) void fwd_kernel(FwdArgs a) {
+__global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdArgs a) {
     constexpr int KD = D / 16;            // k-steps of S^T = K Q^T
     constexpr int DB = (D + 31) / 32;     // 32-row blocks of O^T
     constexpr int NB = BN / 32;           // 32-key blocks per tile
