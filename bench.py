@@ -109,9 +109,6 @@ class KernelCalls:
     def fwd(self):
         _lib.check(self.L.mykfa_fwd(ctypes.byref(self.fp), self.stream))
 
-    def preprocess(self):
-        _lib.check(self.L.mykfa_bwd_preprocess(ctypes.byref(self.bp), self.stream))
-
     def dkdv(self):
         _lib.check(self.L.mykfa_bwd_dkdv(ctypes.byref(self.bp), self.stream))
 
@@ -191,12 +188,12 @@ def measure_prefill(w, steps: int, warmup: int, backward: bool, use_graph: bool 
     reps = max(steps, 10)
     kern = {"fwd": time_events(kc.fwd, reps)}
     if backward:
-        kern["bwd_preprocess"] = time_events(kc.preprocess, reps)
-        kern["bwd_dkdv"] = time_events(kc.dkdv, reps)
+        # The step's backward is dQ (which also computes delta = rowsum(dO * O)) then dK/dV.
         kern["bwd_dq"] = time_events(kc.dq_, reps)
+        kern["bwd_dkdv"] = time_events(kc.dkdv, reps)
     # Algorithmic FLOPs per launch (convention split: fwd = 2 products; of the 5 backward
     # products, dK/dV's kernel owns S, dP, dV, dK = 2.0 F_fwd and dQ's owns dQ = 0.5 F_fwd).
-    algo = {"fwd": w.fwd_flops, "bwd_dkdv": 2.0 * w.fwd_flops, "bwd_dq": 0.5 * w.fwd_flops, "bwd_preprocess": 0.0}
+    algo = {"fwd": w.fwd_flops, "bwd_dkdv": 2.0 * w.fwd_flops, "bwd_dq": 0.5 * w.fwd_flops}
     del inp, step, kc
     return ms, flops, kern, algo
 

@@ -174,11 +174,12 @@ int mykfa_fwd(const mykfa_fwd_params* p, mykfa_stream_t stream);
  * flash_attn.py:215-216). */
 int mykfa_bwd_preprocess(const mykfa_bwd_params* p, mykfa_stream_t stream);
 /* dK, dV summed over each GQA group (replaces _bwd_dkdv_kernel, flash_attn.py:264-314).
- * Reads delta: run mykfa_bwd_preprocess first on the same stream. */
+ * Reads delta: run mykfa_bwd_preprocess or mykfa_bwd_dq first on the same stream. */
 int mykfa_bwd_dkdv(const mykfa_bwd_params* p, mykfa_stream_t stream);
-/* dQ (replaces the dQ part of _bwd_dq_kernel, flash_attn.py:181-230). Reads delta. */
+/* dQ (replaces _bwd_dq_kernel, flash_attn.py:181-230, with its fused delta preprocess,
+ * :215-216): computes delta = rowsum(dO * O) itself and writes it to p->delta. */
 int mykfa_bwd_dq(const mykfa_bwd_params* p, mykfa_stream_t stream);
-/* preprocess, dK/dV and dQ in stream order (replaces _backward, flash_attn.py:376-406). */
+/* dQ (with delta) then dK/dV in stream order (replaces _backward, flash_attn.py:376-406). */
 int mykfa_bwd(const mykfa_bwd_params* p, mykfa_stream_t stream);
 
 /* ---- KV-cache decode (split-K) ------------------------------------------------------ */

@@ -214,11 +214,10 @@ int mykfa_bwd_dq(const mykfa_bwd_params* p, mykfa_stream_t stream) {
 }
 
 int mykfa_bwd(const mykfa_bwd_params* p, mykfa_stream_t stream) {
-    int rc = mykfa_bwd_preprocess(p, stream);
+    // dQ first: it computes delta (the preprocess) itself and writes it for dK/dV.
+    int rc = mykfa_bwd_dq(p, stream);
     if (rc) return rc;
-    rc = mykfa_bwd_dkdv(p, stream);
-    if (rc) return rc;
-    return mykfa_bwd_dq(p, stream);
+    return mykfa_bwd_dkdv(p, stream);
 }
 
 int mykfa_decode_num_splits(int32_t batch, int32_t num_kv_heads, int32_t capacity) {

@@ -410,11 +410,26 @@ __global__ __launch_bounds__(NW * 64) void bwd_dq_kernel(BwdArgs a) {
             doop[kk] = q_ok ? ld16(dop + 16 * kk + 8 * g) : z;
         }
     }
+    // delta = rowsum(dO * O) of this wave's rows (flash_attn.py:215-216), from the dO operand
+    // already in registers and the matching O chunks: lanes l32 and l32 + 32 hold the two halves
+    // of a row. Written out for the dK/dV pass, which runs after this one.
     float lse_q = INFINITY, del_q = 0.f;
+    {
+        const uint16_t* op = a.o + (int64_t)b * a.obs + (qs.tok0 + qi) * a.ots + (int64_t)h * a.ohs;
+        float part = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < KD; ++kk) {
+            s16x8 ov = {0, 0, 0, 0, 0, 0, 0, 0};
+            if (q_ok) ov = ld16(op + 16 * kk + 8 * g);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) part += T::to_float((uint16_t)ov[i]) * T::to_float((uint16_t)doop[kk][i]);
+        }
+        del_q = sum_halves(part);
+    }
     if (q_ok) {
         const int64_t off = (int64_t)h * a.lse_hs + qs.row0 + qi;
         lse_q = a.lse[off];
-        del_q = a.delta[off];
+        if (g == 0) a.delta[off] = del_q;
     }
     wait_vmcnt<0>();  // Q, dO, lse, delta landed before the ring's loads share the counter
 
