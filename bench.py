@@ -284,6 +284,24 @@ def cpu_baseline(w, budget_s: float = 12.0):
             "seconds": round(t_total, 3)}
 
 
+# --- HBM traffic from the committed rocprofv3 summary -------------------------------------------------
+
+def profiled_traffic(kernel: str, profile: str = "cfg2_fwdbwd"):
+    """HBM bytes per dispatch of `kernel` (a kernels_ms key) as measured by the two
+    copy-calibrated rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) summarized in
+    profiles/<profile>_hbm_traffic.txt, whose 'traffic_bytes <kernel> <bytes>' lines carry the
+    figures; None when the summary is absent."""
+    try:
+        with open(os.path.join(ROOT, "profiles", f"{profile}_hbm_traffic.txt")) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) == 3 and parts[0] == "traffic_bytes" and parts[1] == kernel:
+                    return int(parts[2])
+    except OSError:
+        pass
+    return None
+
+
 # --- main -------------------------------------------------------------------------------------------
 
 
@@ -295,6 +313,7 @@ def main():
     ap.add_argument("--workload", default="cfg2")
     ap.add_argument("--quick", action="store_true", help="headline only: no other configs, no CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--decode-only", action="store_true", help="only the decode configs (for profiling)")
     ap.add_argument("--eager", action="store_true", help="time eager calls instead of graph replays")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run a plain 256 MiB fp32 copy kernel 3 times (reads and writes 2^28 bytes "
@@ -316,6 +335,16 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     W = workloads()
+    if args.decode_only:
+        # The decode workloads alone (for profiling their kernels); not the contract line.
+        out = {}
+        for name in ("cfg5", "cfg5_mtp"):
+            wk = W[name]
+            m, kk, splits = measure_decode(wk, args.steps, args.warmup)
+            out[name] = {"ms": round(m, 5), "GB/s": round(wk.decode_bytes / (m * 1e-3) / 1e9, 1), "splits": splits,
+                         "kernel_ms": {k: round(v, 5) for k, v in kk.items()}}
+        print(json.dumps({"decode_only": out}), flush=True)
+        return
     w = W[args.workload]
     log(f"headline {w.name}: fwd+bwd, steps={args.steps} warmup={args.warmup}")
     torch.cuda.synchronize()
@@ -342,9 +371,16 @@ def main():
             log(f"config {wk.name} decode")
             m, kk, splits = measure_decode(wk, max(10, args.steps // 2), 3)
             gbs = wk.decode_bytes / (m * 1e-3) / 1e9
+            # Roofline of the split-K kernel: the step's algorithmic bytes (each K/V byte once per
+            # GQA group, q, O, LSE) over its own average duration.
+            kgbs = wk.decode_bytes / (kk["decode_splitk"] * 1e-3) / 1e9
             configs[name] = {"workload": wk.name, "ms": round(m, 5), "GB/s": round(gbs, 1),
                              "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "bytes": int(wk.decode_bytes),
-                             "splits": splits, "kernel_ms": {k: round(v, 5) for k, v in kk.items()}}
+                             "splits": splits, "kernel_ms": {k: round(v, 5) for k, v in kk.items()},
+                             "roofline": {"kernel": "decode_splitk", "bound": "hbm", "achieved": round(kgbs, 1),
+                                          "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(kgbs / HBM_PEAK_GBS, 4),
+                                          "traffic": profiled_traffic("decode_splitk", "cfg5_decode")
+                                          if name == "cfg5" else None}}
             log(f"  {m * 1e3:.1f} us, {gbs:.0f} GB/s; kernels (ms): " + ", ".join(f"{k}={v:.4f}" for k, v in kk.items()))
     cpu = None
     if not (args.quick or args.no_cpu):
@@ -369,7 +405,8 @@ def main():
                    "timing": "eager" if args.eager else "hipgraph replay", "parallelism": "none (1 GPU)"},
         "frac_of_bf16_peak": round(value / BF16_PEAK_TFLOPS, 4),
         "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2), "peak": BF16_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
+                     "traffic": profiled_traffic(dom),
                      "kernel_ms": round(kern[dom], 5)},
         "kernels_ms": {k: round(v, 5) for k, v in kern.items()},
         "cpu_baseline": cpu,
