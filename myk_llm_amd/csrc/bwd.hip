@@ -247,6 +247,20 @@ __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
             s = T::mfma32(lds_row_op<D>(Qs, 0, l32, g, kk), kop[kk], s);
             dp = T::mfma32(lds_row_op<D>(DOs, 0, l32, g, kk), vop[kk], dp);
         }
+        // Transposed operands of dV/dK, read now so their latency hides under the VALU work
+        // (D <= 128; at D = 256 the registers are not there).
+        constexpr bool PF = D <= 128;
+        s16x8 dot_op[PF ? DB : 1][2], qt_op[PF ? DB : 1][2];
+        if constexpr (PF) {
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+                    dot_op[db][kb] = lds_tr_op<D>(DOs, db, kb, lane);
+                    qt_op[db][kb] = lds_tr_op<D>(Qs, db, kb, lane);
+                }
+            __builtin_amdgcn_sched_barrier(0);
+        }
         const int key = nw0 + l32;
         // Register r = 8 kb + i holds query row m0 + 16 kb + 8 g + i; its lse / delta sit at
         // floats [16 kb + 8 g + i] / [32 + 16 kb + 8 g + i] of the stage.
@@ -294,8 +308,13 @@ __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
         for (int db = 0; db < DB; ++db)
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
-                dv[db] = T::mfma32(lds_tr_op<D>(DOs, db, kb, lane), pb[kb], dv[db]);
-                dk[db] = T::mfma32(lds_tr_op<D>(Qs, db, kb, lane), dsb[kb], dk[db]);
+                if constexpr (PF) {
+                    dv[db] = T::mfma32(dot_op[db][kb], pb[kb], dv[db]);
+                    dk[db] = T::mfma32(qt_op[db][kb], dsb[kb], dk[db]);
+                } else {
+                    dv[db] = T::mfma32(lds_tr_op<D>(DOs, db, kb, lane), pb[kb], dv[db]);
+                    dk[db] = T::mfma32(lds_tr_op<D>(Qs, db, kb, lane), dsb[kb], dk[db]);
+                }
             }
     }
 
@@ -459,6 +478,16 @@ __global__ __launch_bounds__(NW * 64) void bwd_dq_kernel(BwdArgs a) {
         const bool masked = !(n0 >= wr.mid_lo && n0 + BN <= wr.mid_hi);
         const uint16_t* Ks = smem[t % STAGES][0];
         const uint16_t* Vs = smem[t % STAGES][1];
+        // K^T operands of dQ, read first so their latency hides under the softmax work
+        // (D <= 64; above, the registers are not there).
+        constexpr bool PF = D <= 64;
+        s16x8 kt_op[PF ? DB : 1][KB];
+        if constexpr (PF) {
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int kb = 0; kb < KB; ++kb) kt_op[db][kb] = lds_tr_op<D>(Ks, db, kb, lane);
+        }
         s16x8 dsb[KB];
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
@@ -493,7 +522,10 @@ __global__ __launch_bounds__(NW * 64) void bwd_dq_kernel(BwdArgs a) {
 #pragma unroll
         for (int db = 0; db < DB; ++db)
 #pragma unroll
-            for (int kb = 0; kb < KB; ++kb) acc[db] = T::mfma32(lds_tr_op<D>(Ks, db, kb, lane), dsb[kb], acc[db]);
+            for (int kb = 0; kb < KB; ++kb) {
+                if constexpr (PF) acc[db] = T::mfma32(kt_op[db][kb], dsb[kb], acc[db]);
+                else acc[db] = T::mfma32(lds_tr_op<D>(Ks, db, kb, lane), dsb[kb], acc[db]);
+            }
     }
 
     if (q_ok) {
