@@ -136,8 +136,50 @@ def test_backward_and_decode_validation(L):
     assert L.mykfa_decode(ctypes.byref(d), None, 0, None) == _lib.ERR_WORKSPACE
 
 
+def test_buffer_span_limits(L):
+    """Rows of one (sequence, head) are addressed through a 32-bit buffer range: token strides
+    above 2^24 elements and row spans above 2 GiB are rejected as unsupported."""
+    p = good_fwd()
+    p.k_token_stride = (1 << 24) + 8
+    assert L.mykfa_validate_fwd(ctypes.byref(p)) == _lib.ERR_UNSUPPORTED
+    assert b"2^24" in L.mykfa_last_error()
+    p = good_fwd()
+    p.k_token_stride, p.k_batch_stride = 1 << 20, (1 << 20) * 2048
+    p.max_seqlen_k = 2048  # (2047 * 2^20 + 64) * 2 bytes > 2 GiB
+    assert L.mykfa_validate_fwd(ctypes.byref(p)) == _lib.ERR_UNSUPPORTED
+    assert b"2 GiB" in L.mykfa_last_error()
+    p.max_seqlen_k = 1000  # (999 * 2^20 + 64) * 2 bytes < 2 GiB
+    assert L.mykfa_validate_fwd(ctypes.byref(p)) == _lib.OK
+
+
+def test_decode_new_key_rules(L):
+    """seqlen_new counts keys after seqused_k[b]; k_new / v_new (both or neither) are written
+    into the caches by the decode itself."""
+    d = _lib.DecodeParams()
+    d.fwd = good_fwd()
+    d.seqlen_new = -1
+    assert L.mykfa_validate_decode(ctypes.byref(d)) == _lib.ERR_INVALID
+    d.seqlen_new = 4
+    assert L.mykfa_validate_decode(ctypes.byref(d)) == _lib.ERR_INVALID  # needs seqused_k
+    assert b"seqused_k" in L.mykfa_last_error()
+    d.fwd.seqused_k = 0x60000
+    assert L.mykfa_validate_decode(ctypes.byref(d)) == _lib.OK  # rows already appended
+    d.k_new = 0x70000
+    assert L.mykfa_validate_decode(ctypes.byref(d)) == _lib.ERR_INVALID  # v_new missing
+    d.v_new = 0x80000
+    d.kn_batch_stride, d.kn_token_stride, d.kn_head_stride = 4 * 2 * 64, 2 * 64, 64
+    d.vn_batch_stride, d.vn_token_stride, d.vn_head_stride = 4 * 2 * 64, 2 * 64, 64
+    assert L.mykfa_validate_decode(ctypes.byref(d)) == _lib.OK
+    d.k_new = 0x70008
+    assert L.mykfa_validate_decode(ctypes.byref(d)) == _lib.ERR_INVALID
+    assert b"k_new" in L.mykfa_last_error()
+
+
 def test_decode_split_heuristic(L):
     assert L.mykfa_decode_num_splits(64, 4, 16388) >= 8  # fills the chip with 256 (seq, head) pairs
+    # About 352 keys per split on long caches; at least ~2048 workgroups for short ones.
+    assert L.mykfa_decode_num_splits(64, 4, 16384) == 47
+    assert L.mykfa_decode_num_splits(8, 4, 4096) == 32  # 4096 / 128 keys, below the 256-split fill
     assert L.mykfa_decode_num_splits(1, 1, 100) == 1  # short caches are not split
     for b, h, c in [(1, 1, 1 << 20), (512, 8, 4096), (64, 4, 256)]:
         s = L.mykfa_decode_num_splits(b, h, c)
