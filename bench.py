@@ -128,7 +128,7 @@ class DecodeCalls:
         fp = fa._fwd_params(q, kc, vc, self.out, self.lse, None, None, lens, nq, kc.shape[1], scale, wl, wr)
         self.dp = _lib.DecodeParams()
         self.dp.fwd = fp
-        self.dp.num_splits = self.L.mykfa_decode_num_splits(b, kc.shape[2], kc.shape[1])
+        self.dp.num_splits = self.L.mykfa_decode_num_splits(b, h, kc.shape[2], nq, kc.shape[1])
         n = self.L.mykfa_decode_workspace_size(b, h, nq, d, self.dp.num_splits)
         self.ws = torch.empty(max(n, 16), dtype=torch.uint8, device=q.device)
         self.keep = [q, kc, vc, lens]

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define MYKFA_ABI_VERSION 2
+#define MYKFA_ABI_VERSION 3
 #define MYKFA_UNBOUNDED (1 << 30) /* flash_attn.py:32 (_UNBOUNDED) */
 
 /* Status codes. */
@@ -183,8 +183,11 @@ int mykfa_bwd_dq(const mykfa_bwd_params* p, mykfa_stream_t stream);
 int mykfa_bwd(const mykfa_bwd_params* p, mykfa_stream_t stream);
 
 /* ---- KV-cache decode (split-K) ------------------------------------------------------ */
-/* Split count the library would pick for this shape (>= 1). */
-int mykfa_decode_num_splits(int32_t batch, int32_t num_kv_heads, int32_t capacity);
+/* Split count the library would pick for this shape (>= 1): about 88 keys per split per query
+ * row of a KV head (352 for one query of a 4-head group), enough workgroups to fill the chip,
+ * at least 128 keys per split, never a multiple of the 8 XCDs. */
+int mykfa_decode_num_splits(int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t seqlen_q,
+                            int32_t capacity);
 /* Bytes of workspace mykfa_decode needs for this shape and split count. */
 size_t mykfa_decode_workspace_size(int32_t batch, int32_t num_heads, int32_t seqlen_q,
                                    int32_t head_dim, int32_t num_splits);

@@ -165,7 +165,8 @@ hipStream_t as_stream(mykfa_stream_t s) { return reinterpret_cast<hipStream_t>(s
 
 int choose_splits(const mykfa_decode_params* p) {
     return p->num_splits > 0 ? p->num_splits
-                             : mykfa::decode_default_splits(p->fwd.batch, p->fwd.num_kv_heads, p->fwd.max_seqlen_k);
+                             : mykfa::decode_default_splits(p->fwd.batch, p->fwd.num_heads, p->fwd.num_kv_heads,
+                                                            p->fwd.max_seqlen_q, p->fwd.max_seqlen_k);
 }
 
 }  // namespace
@@ -220,8 +221,9 @@ int mykfa_bwd(const mykfa_bwd_params* p, mykfa_stream_t stream) {
     return mykfa_bwd_dkdv(p, stream);
 }
 
-int mykfa_decode_num_splits(int32_t batch, int32_t num_kv_heads, int32_t capacity) {
-    return mykfa::decode_default_splits(batch, num_kv_heads, capacity);
+int mykfa_decode_num_splits(int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t seqlen_q,
+                            int32_t capacity) {
+    return mykfa::decode_default_splits(batch, num_heads, num_kv_heads, seqlen_q, capacity);
 }
 
 size_t mykfa_decode_workspace_size(int32_t batch, int32_t num_heads, int32_t seqlen_q, int32_t head_dim,

@@ -500,20 +500,29 @@ size_t decode_workspace_bytes(int batch, int num_heads, int seqlen_q, int head_d
     return (size_t)num_splits * rows * ((size_t)head_dim + 1) * sizeof(float);
 }
 
-int decode_default_splits(int batch, int num_kv_heads, int capacity) {
-    // About 352 keys per split (measured best on full 16K caches: long enough to stream, short
-    // enough to balance), raised so that full caches give at least ~2048 workgroups (each
-    // kWaves KV heads of one sequence) on the 256-CU chip, and capped at 128 keys per split.
-    const long long heads = num_kv_heads > 0 ? num_kv_heads : 1;
-    const long long pairs = (long long)(batch > 0 ? batch : 1) * ((heads + kWaves - 1) / kWaves);
+int decode_default_splits(int batch, int num_heads, int num_kv_heads, int seqlen_q, int capacity) {
+    // Each split writes an fp32 partial row per query row that the merge reads back, so the
+    // keys per split grow with the query rows of a KV head: about 88 per row (352 for one query
+    // of a 4-head group, ~1400 for the 4-query draft), measured best on full 16K caches. Then at
+    // least ~512 workgroups (each kWaves KV-head units of one sequence) for short batches, at
+    // least 128 keys per split, and never a multiple of the 8 XCDs: the workgroups of split s of
+    // every sequence would then all run on one XCD, idling the XCDs of the late splits.
+    const long long kvh = num_kv_heads > 0 ? num_kv_heads : 1;
+    const long long group = num_heads > 0 ? (num_heads + kvh - 1) / kvh : 1;
+    long long rows = group * (seqlen_q > 0 ? seqlen_q : 1);
+    const long long row_tiles = (rows + 15) / 16;
+    rows = rows < 4 ? 4 : (rows > 16 ? 16 : rows);
+    const long long pairs = (long long)(batch > 0 ? batch : 1) * ((kvh * row_tiles + kWaves - 1) / kWaves);
     const long long cap = capacity > 0 ? capacity : 1;
-    long long splits = (cap + 351) / 352;
-    const long long fill = (2048 + pairs - 1) / pairs;
+    const long long chunk = 88 * rows;
+    long long splits = (cap + chunk - 1) / chunk;
+    const long long fill = (512 + pairs - 1) / pairs;
     if (splits < fill) splits = fill;
     const long long max_by_len = (cap + 127) / 128;
     if (splits > max_by_len) splits = max_by_len;
-    if (splits > 1024) splits = 1024;
+    if (splits > 1023) splits = 1023;
     if (splits < 1) splits = 1;
+    if (splits > 1 && splits % kXcds == 0) ++splits;
     return (int)splits;
 }
 

@@ -17,7 +17,7 @@ hipError_t launch_bwd_dq(const mykfa_bwd_params& p, hipStream_t stream);
 // Split-K decode. The workspace holds, per (split, batch, head, query): D fp32 partial
 // outputs, then one fp32 partial lse per (split, batch, head, query).
 size_t decode_workspace_bytes(int batch, int num_heads, int seqlen_q, int head_dim, int num_splits);
-int decode_default_splits(int batch, int num_kv_heads, int capacity);
+int decode_default_splits(int batch, int num_heads, int num_kv_heads, int seqlen_q, int capacity);
 hipError_t launch_decode_splitk(const mykfa_decode_params& p, int num_splits, void* ws, hipStream_t stream);
 hipError_t launch_decode_merge(const mykfa_decode_params& p, int num_splits, const void* ws,
                                hipStream_t stream);

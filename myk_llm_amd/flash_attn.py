@@ -172,7 +172,7 @@ def _decode_launch(L, p: _lib.FwdParams, device: torch.device, k_new: Optional[T
     k_new / v_new the decode first writes them into the caches after seqused_k[b]."""
     d = _lib.DecodeParams()
     d.fwd = p
-    splits = L.mykfa_decode_num_splits(p.batch, p.num_kv_heads, p.max_seqlen_k)
+    splits = L.mykfa_decode_num_splits(p.batch, p.num_heads, p.num_kv_heads, p.max_seqlen_q, p.max_seqlen_k)
     d.num_splits = splits
     if k_new is not None:
         d.seqlen_new = k_new.shape[1]

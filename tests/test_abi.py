@@ -33,7 +33,7 @@ def test_every_declared_symbol_is_exported_and_bound(L):
 
 
 def test_version_and_struct_sizes(L):
-    assert L.mykfa_abi_version() == _lib.ABI_VERSION == 2
+    assert L.mykfa_abi_version() == _lib.ABI_VERSION == 3
     assert b"gfx950" in L.mykfa_version()
     assert L.mykfa_sizeof_fwd_params() == ctypes.sizeof(_lib.FwdParams)
     assert L.mykfa_sizeof_bwd_params() == ctypes.sizeof(_lib.BwdParams)
@@ -176,14 +176,17 @@ def test_decode_new_key_rules(L):
 
 
 def test_decode_split_heuristic(L):
-    assert L.mykfa_decode_num_splits(64, 4, 16388) >= 8  # fills the chip with 256 (seq, head) pairs
-    # About 352 keys per split on long caches; at least ~2048 workgroups for short ones.
-    assert L.mykfa_decode_num_splits(64, 4, 16384) == 47
-    assert L.mykfa_decode_num_splits(8, 4, 4096) == 32  # 4096 / 128 keys, below the 256-split fill
-    assert L.mykfa_decode_num_splits(1, 1, 100) == 1  # short caches are not split
-    for b, h, c in [(1, 1, 1 << 20), (512, 8, 4096), (64, 4, 256)]:
-        s = L.mykfa_decode_num_splits(b, h, c)
-        assert 1 <= s <= 1024
+    # One query of a 4-head group over full 16K caches: ~352 keys per split (47, odd).
+    assert L.mykfa_decode_num_splits(64, 16, 4, 1, 16384) == 47
+    # The 4-query draft: 16 rows per KV head -> ~1408 keys per split, 12 splits.
+    assert L.mykfa_decode_num_splits(64, 16, 4, 4, 16384) == 12
+    # Never a multiple of the 8 XCDs; short caches are not split; bounds hold.
+    # 8 sequences fill the chip only at 64 splits, capped at 4096 / 128 keys = 32, bumped to 33.
+    assert L.mykfa_decode_num_splits(8, 32, 4, 1, 4096) == 33
+    assert L.mykfa_decode_num_splits(1, 1, 1, 1, 100) == 1
+    for args in [(1, 8, 1, 1, 1 << 20), (512, 32, 8, 2, 4096), (64, 4, 4, 1, 256), (3, 64, 8, 16, 9000)]:
+        s = L.mykfa_decode_num_splits(*args)
+        assert 1 <= s <= 1024 and (s == 1 or s % 8 != 0)
 
 
 def test_kv_append_validation(L):
