@@ -5,8 +5,12 @@
 One "step" is one pass of the hot path over one batch of synthetic input. The headline
 workload is BASELINE config 2 (GQA varlen causal, 8 packed documents, 8248 tokens, Hq=16,
 Hkv=4, D=64, bf16), run as forward + backward through the public API (the north-star
-target is fwd+bwd on this 8K-token GQA varlen shape). The step is captured once in a HIP
-graph and replayed, so host-side launch overhead does not pollute a ~100 us workload.
+target is fwd+bwd on this 8K-token GQA varlen shape). Prefill steps are timed as the
+reference times them (scripts/benchmark_attention.py:31-40): eager public-API calls, HIP
+events around the repeats; the host enqueues a step (~160 us) faster than the GPU runs it,
+so the GPU never waits. --graph replays a captured HIP graph instead (ROCm 7 adds ~7 us
+between graph kernel nodes, which back-to-back eager launches do not). Decode steps are
+graph replays, as in the reference's scripts/benchmark_decode.py:149-157.
 FLOPs follow the reference's convention (scripts/benchmark_attention.py:49-50, 86):
 F_fwd = 4 * visible pairs * Hq * D, F_fwd+bwd = 3.5 * F_fwd.
 
@@ -169,7 +173,7 @@ def attention_step(w, inp, backward: bool):
     return step
 
 
-def measure_prefill(w, steps: int, warmup: int, backward: bool, use_graph: bool = True):
+def measure_prefill(w, steps: int, warmup: int, backward: bool, use_graph: bool = False):
     inp = make_inputs(w, device="cuda", with_grad_out=backward)
     step = attention_step(w, inp, backward)
     if use_graph:
@@ -314,7 +318,7 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only: no other configs, no CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-only", action="store_true", help="only the decode configs (for profiling)")
-    ap.add_argument("--eager", action="store_true", help="time eager calls instead of graph replays")
+    ap.add_argument("--graph", action="store_true", help="time prefill steps as HIP graph replays instead of eager calls")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run a plain 256 MiB fp32 copy kernel 3 times (reads and writes 2^28 bytes "
                          "each), the reference dispatch for scaling FETCH_SIZE / WRITE_SIZE counters")
@@ -348,7 +352,7 @@ def main():
     w = W[args.workload]
     log(f"headline {w.name}: fwd+bwd, steps={args.steps} warmup={args.warmup}")
     torch.cuda.synchronize()
-    ms, flops, kern, algo = measure_prefill(w, args.steps, args.warmup, backward=True, use_graph=not args.eager)
+    ms, flops, kern, algo = measure_prefill(w, args.steps, args.warmup, backward=True, use_graph=args.graph)
     value = flops / (ms * 1e-3) / 1e12
     dom = max((k for k in kern if algo.get(k, 0) > 0), key=lambda k: kern[k])
     achieved = algo[dom] / (kern[dom] * 1e-3) / 1e12
@@ -359,7 +363,7 @@ def main():
             wk = W[name]
             for bwd in ((False, True) if name != "cfg2" else (False,)):
                 log(f"config {wk.name} {'fwd+bwd' if bwd else 'fwd'}")
-                m, f, kk, _ = measure_prefill(wk, max(10, args.steps // 2), 3, backward=bwd)
+                m, f, kk, _ = measure_prefill(wk, max(10, args.steps // 2), 3, backward=bwd, use_graph=args.graph)
                 t = f / (m * 1e-3) / 1e12
                 configs[f"{name}_{'fwdbwd' if bwd else 'fwd'}"] = {
                     "workload": wk.name, "ms": round(m, 5), "TFLOP/s": round(t, 2),
@@ -402,7 +406,7 @@ def main():
         "data": "synthetic (seeded N(0,1) q/k/v/dO, BASELINE config recipes)",
         "config": {"workload": w.name, "pass": "fwd+bwd", "tokens": sum(w.lengths), "docs": len(w.lengths),
                    "heads": w.heads, "kv_heads": w.kv_heads, "head_dim": w.head_dim,
-                   "timing": "eager" if args.eager else "hipgraph replay", "parallelism": "none (1 GPU)"},
+                   "timing": "hipgraph replay" if args.graph else "eager calls, HIP events", "parallelism": "none (1 GPU)"},
         "frac_of_bf16_peak": round(value / BF16_PEAK_TFLOPS, 4),
         "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),

@@ -651,8 +651,8 @@ hipError_t dq_dtype(const BwdArgs& a, int D, hipStream_t s) {
     switch (D) {
         case 16: return dq_launch<16, 64, 4, 4, T>(a, s);
         case 32: return dq_launch<32, 64, 4, 4, T>(a, s);
-        case 64: return dq_launch<64, 64, 8, 4, T>(a, s);
-        case 128: return dq_launch<128, 64, 8, 3, T>(a, s);
+        case 64: return dq_launch<64, 64, 4, 4, T>(a, s);
+        case 128: return dq_launch<128, 64, 4, 2, T>(a, s);
         case 256: return dq_launch<256, 32, 4, 3, T>(a, s);
         default: return hipErrorInvalidValue;
     }

@@ -312,6 +312,42 @@ inline long long block_grid_size(int nblk, int groups, int seqs) {
     return (long long)((nblk + kXcdChunk - 1) / kXcdChunk) * kXcdChunk * groups * seqs;
 }
 
+// ---- split ranks: the longest causal chains run as two workgroups ---------------------------
+// Under a causal mask block rank r carries a serial chain of about gx - r tiles (rank 0 is the
+// longest), and the kernel cannot end before its longest chain does. When that chain is longer
+// than the chip's share of the total work, the first sr ranks each run as two workgroups
+// ("parts") over the two halves of the chain; the parts write fp32 partials to a workspace
+// slot and a small fixup kernel combines them. Extended rank e < 2 sr is (rank e / 2, part
+// e % 2); e >= 2 sr is rank e - sr, unsplit. Slot of (rank < sr, sequence, group):
+// (rank * seqs + seq) * groups + group, two parts each.
+struct SplitRank {
+    int rank, part;  // part -1: unsplit
+};
+__device__ inline SplitRank split_rank(int e, int sr) {
+    if (e < 2 * sr) return {e >> 1, e & 1};
+    return {e - sr, -1};
+}
+inline int64_t split_slot(int rank, int seq, int group, int seqs, int groups) {
+    return ((int64_t)rank * seqs + seq) * groups + group;
+}
+__device__ inline int64_t split_slot_d(int rank, int seq, int group, int seqs, int groups) {
+    return ((int64_t)rank * seqs + seq) * groups + group;
+}
+
+// Compute units of the current device (256 on MI355X; also the answer without a device, so
+// that workspace sizes can be asked for on a host without one).
+int device_cu_count();
+
+// Number of ranks to split. gx ranks of `blk` rows each; rows = all query (or key) rows of the
+// problem (varlen: the packed total; the per-sequence lengths live on the device, so the chip's
+// share of the work is estimated from gx and rows: the geometric mean of its lower bound, one
+// sequence of gx blocks plus one block per other block, and its upper bound, every block a
+// longest-sequence block). The two parts' partials take 2 * part_bytes per slot; the plan keeps
+// the workspace under kSplitWorkspaceCap.
+constexpr size_t kSplitWorkspaceCap = size_t(256) << 20;
+int split_ranks(int gx, int seqs, int groups, int64_t rows, int blk, bool varlen, bool causal, int wgs_per_cu,
+                size_t part_bytes);
+
 // ---- sequences --------------------------------------------------------------------------
 
 struct SeqInfo {

@@ -1,6 +1,6 @@
 // Prefill forward: O and base-2 LSE (replaces _fwd_kernel, flash_attn.py:106-154).
 //
-// Work decomposition. A workgroup is NW waves (8, or 4 for small/large head_dim); every wave
+// Work decomposition. A workgroup is NW waves (4); every wave
 // owns 32 query rows of one head. The workgroup's waves cover `hpw` query heads of ONE GQA
 // group (hpw = gcd(group, NW)) times NW / hpw blocks of 32 consecutive tokens, so each K/V
 // tile staged in LDS serves every query head of the group that the workgroup holds: K/V
@@ -96,6 +96,17 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdArgs a) {
     const i32x4 rsrc[2] = {rows_rsrc(kbase, k_len, a.kts, D), rows_rsrc(vbase, k_len, a.vts, D)};
     const int tstride[2] = {(int)(a.kts * 2), (int)(a.vts * 2)};
 
+    const int ntiles = wg_hi > wg_lo ? (wg_hi - wg_lo + BN - 1) / BN : 0;
+    auto issue = [&](int t) {
+        uint16_t* tiles[2] = {smem[t % STAGES][0], smem[t % STAGES][1]};
+        Ring::issue(rsrc, tstride, tiles, wg_lo + t * BN, wave, lane);
+    };
+    // The ring's first tiles go out before the Q loads, so the two latencies overlap.
+#pragma unroll
+    for (int t = 0; t < STAGES - 1; ++t)
+        if (t < ntiles) issue(t);
+
+
     // Q rows of this wave as the B operand of S^T = K Q^T: lane holds Q[s0 + l32][16kk + 8g + i].
     // A negative scale is applied as |scale| on sign-flipped Q (exact), so the row max can be
     // taken on raw scores.
@@ -112,9 +123,11 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdArgs a) {
             qop[kk] = v ^ flip;
         }
     }
-    // Q must have landed before the ring's loads join the same in-order counter; otherwise
-    // the compiler, unable to count loop-carried loads, drains the counter inside the loop.
+    // Q and the prefetched tiles land together (one memory round trip for the prologue). No
+    // load may stay outstanding into the loop: the compiler cannot count the ring's loads and
+    // would drain the counter inside the loop.
     wait_vmcnt<0>();
+
 
     f32x16 acc[DB];
 #pragma unroll
@@ -122,15 +135,6 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
     float m_i = kNegFloor, l_i = 0.f;
-
-    const int ntiles = wg_hi > wg_lo ? (wg_hi - wg_lo + BN - 1) / BN : 0;
-    auto issue = [&](int t) {
-        uint16_t* tiles[2] = {smem[t % STAGES][0], smem[t % STAGES][1]};
-        Ring::issue(rsrc, tstride, tiles, wg_lo + t * BN, wave, lane);
-    };
-#pragma unroll
-    for (int t = 0; t < STAGES - 1; ++t)
-        if (t < ntiles) issue(t);
 
     for (int t = 0; t < ntiles; ++t) {
         const int n0 = wg_lo + t * BN;
@@ -269,14 +273,18 @@ hipError_t launch_typed(FwdArgs args, int batch, int num_heads, int max_q, hipSt
     return hipGetLastError();
 }
 
-// Tile shapes per head_dim: (keys per tile, waves per workgroup, LDS ring stages).
+// Tile shapes per head_dim: (keys per tile, waves per workgroup, LDS ring stages). Four-wave
+// workgroups, two or more per CU: the waves sharing a SIMD then belong to different
+// workgroups, whose per-tile barriers do not hold them in the same phase, so one wave's MFMAs
+// overlap the other's softmax (measured 15-20% faster than eight-wave workgroups at D = 64
+// and 128).
 template <typename T>
 hipError_t launch_dtype(const FwdArgs& args, int D, int batch, int num_heads, int max_q, hipStream_t s) {
     switch (D) {
         case 16: return launch_typed<16, 64, 4, 4, T>(args, batch, num_heads, max_q, s);
         case 32: return launch_typed<32, 64, 4, 4, T>(args, batch, num_heads, max_q, s);
-        case 64: return launch_typed<64, 64, 8, 4, T>(args, batch, num_heads, max_q, s);
-        case 128: return launch_typed<128, 64, 8, 4, T>(args, batch, num_heads, max_q, s);
+        case 64: return launch_typed<64, 64, 4, 4, T>(args, batch, num_heads, max_q, s);
+        case 128: return launch_typed<128, 64, 4, 2, T>(args, batch, num_heads, max_q, s);
         case 256: return launch_typed<256, 32, 4, 3, T>(args, batch, num_heads, max_q, s);
         default: return hipErrorInvalidValue;
     }
