@@ -121,7 +121,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
     // Key blocks are ranked from the END of each sequence: under a causal mask key block n of
     // a sequence of nblk blocks sees nblk - n query blocks, so equal ranks carry equal work in
     // every sequence and rank 0 (the first key block of the longest sequences) starts first.
-    const BlockCoord bc = block_coord(xcd_logical(blockIdx.x), a.gz, a.gy);
+    const BlockCoord bc = block_coord(xcd_logical(blockIdx.x), a.gz, a.gy, a.cu_k != nullptr);
     if (bc.rank >= a.gx) return;
     const int kvh = bc.group;
     const int b = bc.seq;
@@ -380,7 +380,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_dq_kernel(BwdArgs a) {
     const int l32 = lane & 31, g = lane >> 5;
     const int tpw = NW / a.hpw;
     // Longest causal rows first across all heads and sequences, XCD-grouped.
-    const BlockCoord bc = block_coord(xcd_logical(blockIdx.x), a.gz, a.gy);
+    const BlockCoord bc = block_coord(xcd_logical(blockIdx.x), a.gz, a.gy, a.cu_q != nullptr);
     if (bc.rank >= a.gx) return;
     const int mblk = a.gx - 1 - bc.rank;
     const int h_first = bc.group * a.hpw;
@@ -613,7 +613,7 @@ hipError_t dkdv_launch(BwdArgs a, int num_kv_heads, hipStream_t s) {
     a.gx = (a.seqlen_k + keys_per_wg - 1) / keys_per_wg;
     a.gy = a.batch;
     a.gz = num_kv_heads;
-    const long long n = block_grid_size(a.gx, a.gz, a.gy);
+    const long long n = block_grid_size(a.gx, a.gz, a.gy, a.cu_k != nullptr);
     if (n == 0) return hipSuccess;
     if (n > (1LL << 30)) return hipErrorInvalidConfiguration;
     hipLaunchKernelGGL((bwd_dkdv_kernel<D, NW, STAGES, T>), dim3(xcd_grid((int)n)), dim3(NW * 64), 0, s, a);
@@ -639,7 +639,7 @@ hipError_t dq_launch(BwdArgs a, hipStream_t s) {
     a.gx = (a.seqlen_q + tpw * 32 - 1) / (tpw * 32);
     a.gy = a.batch;
     a.gz = a.num_heads / a.hpw;
-    const long long n = block_grid_size(a.gx, a.gz, a.gy);
+    const long long n = block_grid_size(a.gx, a.gz, a.gy, a.cu_q != nullptr);
     if (n == 0) return hipSuccess;
     if (n > (1LL << 30)) return hipErrorInvalidConfiguration;
     hipLaunchKernelGGL((bwd_dq_kernel<D, BN, NW, STAGES, T>), dim3(xcd_grid((int)n)), dim3(NW * 64), 0, s, a);

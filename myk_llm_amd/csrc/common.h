@@ -280,7 +280,7 @@ __device__ inline void ring_wait(int tiles_after) {
 // query / key blocks of one head, which read the same K/V or Q/dO tiles) executes on one XCD
 // and shares its L2. Logical ids >= n (padding) exit at once.
 constexpr int kXcds = 8;
-constexpr int kXcdChunk = 8;
+constexpr int kXcdChunk = 4;
 __host__ __device__ inline int xcd_grid(int n) {
     const int q = kXcds * kXcdChunk;
     return (n + q - 1) / q * q;
@@ -297,56 +297,39 @@ __device__ inline int xcd_logical(int pid) {
 // the long causal blocks of the last sequences for the tail) while each run of kXcdChunk
 // consecutive blocks of one (group, sequence) still executes on one XCD. Ranks >= the block
 // count (padding) are for the caller to skip.
+//
+// Run j of a (group, sequence) pair is run index R = j * P + pair, which executes on XCD R % 8.
+// For packed (varlen) batches, whose sequences differ in length and so in work, from 8 pairs
+// on P is padded (idle pairs exit at once) to P = 4 (mod 8), so that the runs of
+// a pair alternate between two XCDs, pair % 8 and pair % 8 + 4 (below 8 pairs P stays as it
+// is: the pairs then rotate through 8, 4 or 2 XCDs each and still cover all). With P a multiple of 8
+// every run of a pair lands on one XCD: the XCDs holding the longest sequences then carry most
+// of the work while the others idle (measured: 30% more work on half of the XCDs for 8
+// sequences x 4 KV heads). Spreading a pair over all eight XCDs (P odd) balances the work but
+// costs each XCD's L2 the pair's tiles eight times over, which measured slower; two XCDs per
+// pair, in runs of kXcdChunk = 4 ranks, measured best (5-8% on a skewed varlen batch, within
+// noise on long ones; shorter runs lost up to a quarter to L2 misses). Dense batches, whose
+// pairs all carry the same work, keep P unpadded: every pair on one XCD (2-5% faster there).
 struct BlockCoord {
     int rank, group, seq;
 };
-__device__ inline BlockCoord block_coord(int logical, int groups, int seqs) {
+__host__ __device__ inline int coord_pairs(int groups, int seqs, bool varlen) {
+    const int p = groups * seqs;
+    return (!varlen || p < 8) ? p : p + (12 - p % 8) % 8;
+}
+__device__ inline BlockCoord block_coord(int logical, int groups, int seqs, bool varlen) {
     const int lo = logical % kXcdChunk, rest = logical / kXcdChunk;
+    const int P = coord_pairs(groups, seqs, varlen);
+    const int j = rest / P, pair = rest % P;
     BlockCoord c;
-    c.group = rest % groups;
-    c.seq = (rest / groups) % seqs;
-    c.rank = rest / (groups * seqs) * kXcdChunk + lo;
+    c.group = pair % groups;
+    c.seq = pair / groups;
+    c.rank = pair < groups * seqs ? j * kXcdChunk + lo : 0x3fffffff;  // idle pair: no block
     return c;
 }
-inline long long block_grid_size(int nblk, int groups, int seqs) {
-    return (long long)((nblk + kXcdChunk - 1) / kXcdChunk) * kXcdChunk * groups * seqs;
+inline long long block_grid_size(int nblk, int groups, int seqs, bool varlen) {
+    return (long long)((nblk + kXcdChunk - 1) / kXcdChunk) * kXcdChunk * coord_pairs(groups, seqs, varlen);
 }
-
-// ---- split ranks: the longest causal chains run as two workgroups ---------------------------
-// Under a causal mask block rank r carries a serial chain of about gx - r tiles (rank 0 is the
-// longest), and the kernel cannot end before its longest chain does. When that chain is longer
-// than the chip's share of the total work, the first sr ranks each run as two workgroups
-// ("parts") over the two halves of the chain; the parts write fp32 partials to a workspace
-// slot and a small fixup kernel combines them. Extended rank e < 2 sr is (rank e / 2, part
-// e % 2); e >= 2 sr is rank e - sr, unsplit. Slot of (rank < sr, sequence, group):
-// (rank * seqs + seq) * groups + group, two parts each.
-struct SplitRank {
-    int rank, part;  // part -1: unsplit
-};
-__device__ inline SplitRank split_rank(int e, int sr) {
-    if (e < 2 * sr) return {e >> 1, e & 1};
-    return {e - sr, -1};
-}
-inline int64_t split_slot(int rank, int seq, int group, int seqs, int groups) {
-    return ((int64_t)rank * seqs + seq) * groups + group;
-}
-__device__ inline int64_t split_slot_d(int rank, int seq, int group, int seqs, int groups) {
-    return ((int64_t)rank * seqs + seq) * groups + group;
-}
-
-// Compute units of the current device (256 on MI355X; also the answer without a device, so
-// that workspace sizes can be asked for on a host without one).
-int device_cu_count();
-
-// Number of ranks to split. gx ranks of `blk` rows each; rows = all query (or key) rows of the
-// problem (varlen: the packed total; the per-sequence lengths live on the device, so the chip's
-// share of the work is estimated from gx and rows: the geometric mean of its lower bound, one
-// sequence of gx blocks plus one block per other block, and its upper bound, every block a
-// longest-sequence block). The two parts' partials take 2 * part_bytes per slot; the plan keeps
-// the workspace under kSplitWorkspaceCap.
-constexpr size_t kSplitWorkspaceCap = size_t(256) << 20;
-int split_ranks(int gx, int seqs, int groups, int64_t rows, int blk, bool varlen, bool causal, int wgs_per_cu,
-                size_t part_bytes);
 
 // ---- sequences --------------------------------------------------------------------------
 

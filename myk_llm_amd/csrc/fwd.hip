@@ -57,7 +57,7 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdArgs a) {
     const int tpw = NW / a.hpw;
     // Longest causal rows first across all heads and sequences (flash_attn.py:115 orders
     // within one head only), XCD-grouped.
-    const BlockCoord bc = block_coord(xcd_logical(__builtin_amdgcn_workgroup_id_x()), a.gz, a.gy);
+    const BlockCoord bc = block_coord(xcd_logical(__builtin_amdgcn_workgroup_id_x()), a.gz, a.gy, a.cu_q != nullptr);
     if (bc.rank >= a.gx) return;
     const int mblk = a.gx - 1 - bc.rank;
     const int h_first = bc.group * a.hpw;
@@ -266,7 +266,7 @@ hipError_t launch_typed(FwdArgs args, int batch, int num_heads, int max_q, hipSt
     args.gx = (max_q + tpw * 32 - 1) / (tpw * 32);
     args.gy = batch;
     args.gz = num_heads / args.hpw;
-    const long long n = block_grid_size(args.gx, args.gz, args.gy);
+    const long long n = block_grid_size(args.gx, args.gz, args.gy, args.cu_q != nullptr);
     if (n == 0) return hipSuccess;
     if (n > (1LL << 30)) return hipErrorInvalidConfiguration;
     hipLaunchKernelGGL((fwd_kernel<D, BN, NW, STAGES, T>), dim3(xcd_grid((int)n)), dim3(NW * 64), 0, s, args);
