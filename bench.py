@@ -10,7 +10,9 @@ reference times them (scripts/benchmark_attention.py:31-40): eager public-API ca
 events around the repeats; the host enqueues a step (~160 us) faster than the GPU runs it,
 so the GPU never waits. --graph replays a captured HIP graph instead (ROCm 7 adds ~7 us
 between graph kernel nodes, which back-to-back eager launches do not). Decode steps are
-graph replays, as in the reference's scripts/benchmark_decode.py:149-157.
+graph replays, as in the reference's scripts/benchmark_decode.py:149-157. Every timed region
+follows the W warmup steps and a further ~0.3 s of untimed steps (settle()), so that the
+GPU's clocks have ramped up: the first ~0.2 s of load runs up to 15% slower.
 FLOPs follow the reference's convention (scripts/benchmark_attention.py:49-50, 86):
 F_fwd = 4 * visible pairs * Hq * D, F_fwd+bwd = 3.5 * F_fwd.
 
@@ -48,11 +50,24 @@ def log(*a):
 # --- timing helpers -------------------------------------------------------------------------
 
 
+def settle(fn, seconds: float = 0.3) -> None:
+    """Run fn untimed for about `seconds` of wall time. The GPU's clocks ramp up over the first
+    ~0.1-0.2 s of sustained load: measured on the box, the cfg2 step takes 195 us in its first
+    50 repeats and 170 us afterwards. Steady-state throughput is what a training run sees."""
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(8):
+            fn()
+        torch.cuda.synchronize()
+
+
 def time_events(fn, reps: int, warmup: int = 2) -> float:
-    """Average ms per call of fn (launches on torch's current stream), HIP events around reps."""
+    """Average ms per call of fn (launches on torch's current stream), HIP events around reps,
+    after `warmup` untimed calls and a settle() of the clocks."""
     for _ in range(warmup):
         fn()
-    torch.cuda.synchronize()
+    settle(fn)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(reps):
