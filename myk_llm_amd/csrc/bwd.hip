@@ -220,16 +220,17 @@ __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
             idel += f_hstep;
         }
     };
+    // Every stage is filled up front, and a stage is refilled (tile it + STAGES) as soon as
+    // iteration it has read it, before that iteration's dV/dK products: a tile gets about
+    // STAGES - 1/2 iterations to land rather than STAGES - 1.
 #pragma unroll
-    for (int t = 0; t < STAGES - 1; ++t)
+    for (int t = 0; t < STAGES; ++t)
         if (t < iters) issue();
 
     int cur_tile = 0, cur_stage = 0;
     for (int it = 0; it < iters; ++it) {
-        const int after = iters - 1 - it < STAGES - 2 ? iters - 1 - it : STAGES - 2;
-        ring_wait<LOADS, STAGES>(after);
-        wait_lgkmcnt0();  // this wave's reads of the stage about to be refilled have returned
-        if (it + STAGES - 1 < iters) issue();
+        const int after = iters - 1 - it < STAGES - 1 ? iters - 1 - it : STAGES - 1;
+        ring_wait<LOADS, STAGES + 1>(after);  // tile it landed; up to STAGES - 1 later tiles in flight
         const int m0 = wr.lo + cur_tile * BMQ;
         const bool masked = !(m0 >= wr.mid_lo && m0 + BMQ <= wr.mid_hi);
         const uint16_t* st = ring + cur_stage * STAGE;
@@ -303,6 +304,12 @@ __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
             pb[kb] = __builtin_bit_cast(s16x8, pw);
             dsb[kb] = __builtin_bit_cast(s16x8, dw);
         }
+        // With the transposed operands already in registers the stage is free: refill it now
+        // (this wave's reads of it have returned), ahead of the dV/dK products.
+        if constexpr (PF) {
+            wait_lgkmcnt0();
+            if (it + STAGES < iters) issue();
+        }
         // dV^T += dO^T P, dK^T += Q^T dS.
 #pragma unroll
         for (int db = 0; db < DB; ++db)
@@ -316,6 +323,10 @@ __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
                     dk[db] = T::mfma32(lds_tr_op<D>(Qs, db, kb, lane), dsb[kb], dk[db]);
                 }
             }
+        if constexpr (!PF) {
+            wait_lgkmcnt0();
+            if (it + STAGES < iters) issue();
+        }
     }
 
     // Sum the hpw partials of each key block in a fixed order (waves hs = 1.. into hs = 0).
@@ -651,7 +662,7 @@ hipError_t dq_dtype(const BwdArgs& a, int D, hipStream_t s) {
     switch (D) {
         case 16: return dq_launch<16, 64, 4, 4, T>(a, s);
         case 32: return dq_launch<32, 64, 4, 4, T>(a, s);
-        case 64: return dq_launch<64, 64, 4, 4, T>(a, s);
+        case 64: return dq_launch<64, 32, 4, 4, T>(a, s);
         case 128: return dq_launch<128, 64, 4, 2, T>(a, s);
         case 256: return dq_launch<256, 32, 4, 3, T>(a, s);
         default: return hipErrorInvalidValue;
