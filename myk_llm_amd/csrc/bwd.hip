@@ -1,16 +1,20 @@
 // Backward pass (replaces _bwd_dq_kernel and _bwd_dkdv_kernel, flash_attn.py:157-314).
-// Three launches in stream order, no atomics (results are bitwise deterministic):
-//   1. preprocess: delta = rowsum(dO * O) in fp32                 (flash_attn.py:215-216)
-//   2. dK/dV: one workgroup per 128-key block of one KV head; K and V stay in registers as
-//      MFMA B operands while the workgroup streams the query tiles of EVERY query head of
-//      the GQA group through LDS, so K/V are read once per group (flash_attn.py:300-311).
-//      Per 32-query step a wave computes S = Q K^T and dP = dO V^T (A operands: row reads
-//      of the LDS Q/dO tiles), P = exp2(S * c - lse), dS = P (dP - delta), then
-//      dV^T += dO^T P and dK^T += Q^T dS with dO^T / Q^T taken by the LDS transpose read.
-//   3. dQ: forward-shaped: S^T = K Q^T, dP^T = V dO^T, dS^T = P^T (dP^T - delta), then
-//      dQ^T += K^T dS^T with K^T read transposed from the LDS K tile.
-// All products are 32x32x16 bf16 (or fp16) MFMA with fp32 accumulation; P and dS are
-// rounded to the input type before their products, as in flash_attn.py:177, :257, :260.
+// Two launches in stream order, no atomics (results are bitwise deterministic):
+//   1. dQ: forward-shaped: delta = rowsum(dO * O) for the workgroup's rows first (the
+//      preprocess fused into _bwd_dq_kernel, flash_attn.py:215-216), written for pass 2; then
+//      S^T = K Q^T, dP^T = V dO^T, dS^T = P^T (dP^T - delta), and dQ^T += K^T dS^T with K^T read
+//      transposed from the LDS K tile.
+//   2. dK/dV: one workgroup per 32-key block of one KV head (4 waves = up to 4 query heads of
+//      the GQA group); K and V stay in registers as MFMA B operands while each wave streams
+//      the query tiles of its head through a wave-private LDS ring, so K/V are read once per
+//      group (flash_attn.py:300-311). Per 32-query step a wave computes S = Q K^T and
+//      dP = dO V^T (A operands: row reads of the LDS Q/dO tiles), P = exp2(S * c - lse),
+//      dS = P (dP - delta), then dV^T += dO^T P and dK^T += Q^T dS with dO^T / Q^T taken by the
+//      LDS transpose read.
+// bwd_preprocess_kernel computes delta alone (mykfa_bwd_preprocess), for callers that run
+// dK/dV without dQ. All products are 32x32x16 bf16 (or fp16) MFMA with fp32 accumulation;
+// P and dS are rounded to the input type before their products, as in flash_attn.py:177,
+// :257, :260.
 #include "common.h"
 #include "kernels.h"
 
