@@ -197,31 +197,78 @@ __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
         do_lane[j] = (unsigned)(row * (int)(a.dots * 2) + logical * 16);
     }
     const unsigned f_lane = (unsigned)((lane & 31) * 4);
+    // Issue-side state, advanced by additions only: the addresses of the next tile's first Q,
+    // dO and lse rows, and the bytes from each to the end of the sequence's rows (the
+    // descriptors' ranges: rows at or beyond q_len read 0). After ntiles tiles they move to the
+    // next head of the wave (hpw heads on). delta shares lse's (head, row) layout, so its
+    // address is lse's plus a fixed distance.
+    const uint64_t q_tstep = (uint64_t)(BMQ * qts) * 2, do_tstep = (uint64_t)(BMQ * dots) * 2;
+    const int rows0 = q_len - wr.lo;  // >= 1 whenever a tile is issued
+    const int qb0 = rows0 > 0 ? (int)(((int64_t)(rows0 - 1) * qts + D) * 2) : 0;
+    const int dob0 = rows0 > 0 ? (int)(((int64_t)(rows0 - 1) * dots + D) * 2) : 0;
+    const int fb0 = rows0 * 4;
+    uint64_t hq = reinterpret_cast<uint64_t>(iq + (int64_t)wr.lo * qts);
+    uint64_t hdo = reinterpret_cast<uint64_t>(ido + (int64_t)wr.lo * dots);
+    uint64_t hf = reinterpret_cast<uint64_t>(ilse + wr.lo);
+    const uint64_t dl = reinterpret_cast<uint64_t>(idel) - reinterpret_cast<uint64_t>(ilse);
+    const uint64_t q_hb = (uint64_t)q_hstep * 2, do_hb = (uint64_t)do_hstep * 2, f_hb = (uint64_t)f_hstep * 4;
+    uint64_t tq = hq, tdo = hdo, tf = hf;
+    int qb = qb0, dob = dob0, fb = fb0;
     int iss_tile = 0, iss_stage = 0;
     auto issue = [&]() {
-        const int m0 = wr.lo + iss_tile * BMQ;
         const uint32_t st = ring_lds + iss_stage * (STAGE * 2);
-        // Rows m0.. of the current head; rows at or beyond q_len read 0.
-        const i32x4 rq = rows_rsrc(iq + m0 * qts, q_len - m0, qts, D);
-        const i32x4 rd = rows_rsrc(ido + m0 * dots, q_len - m0, dots, D);
+        const uint32_t fl = st + 2 * TILE * 2;  // lse into floats [0, 32), delta into [32, 64)
+        if constexpr (D <= 128) {
+            const i32x4 rq = buffer_rsrc32(tq, qb);
+            const i32x4 rd = buffer_rsrc32(tdo, dob);
 #pragma unroll
-        for (int j = 0; j < QLOADS; ++j) {
-            dma16(rq, st + j * 1024, q_lane[j]);
-            dma16(rd, st + (TILE + j * 512) * 2, do_lane[j]);
+            for (int j = 0; j < QLOADS; ++j) {
+                dma16(rq, st + j * 1024, q_lane[j]);
+                dma16(rd, st + (TILE + j * 512) * 2, do_lane[j]);
+            }
+            if (lane < 32) dma4(buffer_rsrc32(tf, fb), fl, f_lane);
+            if (lane >= 32) dma4(buffer_rsrc32(tf + dl, fb), fl, f_lane);
+        } else {
+            // Same tiles from the head pointers (the compiler's AGPR rewrite pass crashes on
+            // the incremental form at D = 256).
+            const int m0 = wr.lo + iss_tile * BMQ;
+            const i32x4 rq = rows_rsrc(iq + m0 * qts, q_len - m0, qts, D);
+            const i32x4 rd = rows_rsrc(ido + m0 * dots, q_len - m0, dots, D);
+#pragma unroll
+            for (int j = 0; j < QLOADS; ++j) {
+                dma16(rq, st + j * 1024, q_lane[j]);
+                dma16(rd, st + (TILE + j * 512) * 2, do_lane[j]);
+            }
+            const int64_t fbytes = (int64_t)(q_len - m0) * 4;
+            if (lane < 32) dma4(buffer_rsrc(ilse + m0, fbytes), fl, f_lane);
+            if (lane >= 32) dma4(buffer_rsrc(idel + m0, fbytes), fl, f_lane);
         }
-        // lse into floats [0, 32), delta into [32, 64) of the stage's float area; rows at or
-        // beyond q_len read 0 (their probabilities are masked to 0).
-        const int64_t fbytes = (int64_t)(q_len - m0) * 4;
-        const uint32_t fl = st + 2 * TILE * 2;
-        if (lane < 32) dma4(buffer_rsrc(ilse + m0, fbytes), fl, f_lane);
-        if (lane >= 32) dma4(buffer_rsrc(idel + m0, fbytes), fl, f_lane);
         iss_stage = iss_stage + 1 == STAGES ? 0 : iss_stage + 1;
         if (++iss_tile == ntiles) {
             iss_tile = 0;
-            iq += q_hstep;
-            ido += do_hstep;
-            ilse += f_hstep;
-            idel += f_hstep;
+            if constexpr (D <= 128) {
+                hq += q_hb;
+                hdo += do_hb;
+                hf += f_hb;
+                tq = hq;
+                tdo = hdo;
+                tf = hf;
+                qb = qb0;
+                dob = dob0;
+                fb = fb0;
+            } else {
+                iq += q_hstep;
+                ido += do_hstep;
+                ilse += f_hstep;
+                idel += f_hstep;
+            }
+        } else if constexpr (D <= 128) {
+            tq += q_tstep;
+            tdo += do_tstep;
+            tf += BMQ * 4;
+            qb -= (int)q_tstep;
+            dob -= (int)do_tstep;
+            fb -= BMQ * 4;
         }
     };
     // Every stage is filled up front, and a stage is refilled (tile it + STAGES) as soon as

@@ -202,6 +202,15 @@ __device__ inline i32x4 buffer_rsrc(const void* base, int64_t bytes) {
     r[3] = 0x00020000;
     return r;
 }
+// The same from a wave-uniform address and a byte range already known to fit 31 bits.
+__device__ inline i32x4 buffer_rsrc32(uint64_t a, int bytes) {
+    i32x4 r;
+    r[0] = __builtin_amdgcn_readfirstlane((int32_t)(uint32_t)(a & 0xffffffffu));
+    r[1] = __builtin_amdgcn_readfirstlane((int32_t)(uint32_t)((a >> 32) & 0xffffu));  // stride 0
+    r[2] = __builtin_amdgcn_readfirstlane(bytes);
+    r[3] = 0x00020000;
+    return r;
+}
 // Descriptor over the valid rows [0, rows) of a (rows, D) 16-bit tensor with row stride tstride.
 __device__ inline i32x4 rows_rsrc(const uint16_t* base, int rows, int64_t tstride, int D) {
     return buffer_rsrc(base, rows > 0 ? ((int64_t)(rows - 1) * tstride + D) * 2 : 0);
