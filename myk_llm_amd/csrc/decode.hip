@@ -12,9 +12,12 @@
 // waves of a workgroup read adjacent heads of the same cache rows (contiguous DRAM rows in the
 // usual (batch, token, head, d) layout) and share nothing: no barrier, no cross-wave merge.
 // A wave streams its keys in 32-key tiles through a ring of NBUF register tiles filled by
-// bounds-checked buffer loads (NBUF - 1 tiles in flight while one computes): S^T = K Q^T on
-// 16x16x32 MFMA with K straight from the registers, the online softmax, and O^T += V^T P^T
-// with V staged in wave-private, double-buffered LDS and read back transposed. A wave then
+// bounds-checked buffer loads (NBUF - 1 tiles in flight while one computes). Every load reads
+// whole 128-byte lines (8 lanes per key row of 64 elements): a load in the MFMA operand layout
+// itself would read 16 keys x 64 bytes, two requests per line, which measured 8% slower at the
+// same bytes. The tile then goes through wave-private LDS: K is read back as the A operand of
+// S^T = K Q^T on 16x16x32 MFMA, then the online softmax, and V is read back transposed for
+// O^T += V^T P^T. A wave then
 // writes either the final O/LSE (one split) or an fp32 partial (O, lse) that the merge kernel
 // combines: lse = log2(sum_s 2^lse_s), O = sum_s 2^(lse_s - lse) O_s.
 #include "common.h"
@@ -80,10 +83,14 @@ template <int D, typename T>
 __global__ __launch_bounds__(kThreads) void decode_splitk_kernel(DecodeArgs a) {
     constexpr int KD = D < 32 ? 1 : D / 32;  // 32-wide d steps of S^T (D = 16 pads to 32)
     constexpr int DB = (D + 15) / 16;        // 16-row blocks of O^T
-    constexpr int VPL = kTile * D / 8 / 64 > 0 ? kTile * D / 8 / 64 : 1;  // V chunks per lane
+    constexpr int VPL = kTile * D / 8 / 64;  // 16-byte chunks per lane of a K or V tile
     constexpr int NBUF = decode_nbuf<D>();
-    static_assert(kTile * D / 8 >= 64 && (kTile * D / 8) % 64 == 0, "V tile is whole 64-lane loads");
-    __shared__ __attribute__((aligned(16))) uint16_t vlds[kWaves][2][kTile * D];
+    static_assert(kTile * D / 8 >= 64 && (kTile * D / 8) % 64 == 0, "K/V tile is whole 64-lane loads");
+    // Staging: double-buffered up to D = 64 (16 KB per wave), single above so that two
+    // workgroups still fit a CU (LDS ops of one wave execute in order, so one buffer is safe).
+    constexpr int NPAR = D <= 64 ? 2 : 1;
+    __shared__ __attribute__((aligned(16))) uint16_t klds[kWaves][NPAR][kTile * D];
+    __shared__ __attribute__((aligned(16))) uint16_t vlds[kWaves][NPAR][kTile * D];
 
     const int tid = __builtin_amdgcn_workitem_id_x();
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -162,20 +169,13 @@ __global__ __launch_bounds__(kThreads) void decode_splitk_kernel(DecodeArgs a) {
     // Tile offset of a tile past the split's end: every lane offset plus it lies in
     // [2^31, 2^32), outside any buffer (lane offsets stay below 2^31: 31 token strides at most).
     constexpr unsigned kSkip = 0x80000000u;
-    // Loop-invariant lane offsets inside a tile. K block kb holds keys 8 (rho / 4) + 4 kb +
-    // rho % 4 in its 16 rows (the order of the score registers).
-    unsigned koff[2][KD], voff[VPL];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int kk = 0; kk < KD; ++kk) {
-            const int key = 8 * (l16 >> 2) + 4 * kb + (l16 & 3);
-            const int d0 = 32 * kk + 8 * G;
-            koff[kb][kk] = (unsigned)key * kts2 + (d0 < D ? d0 : 0) * 2;
-        }
+    // Loop-invariant lane offsets inside a tile: chunk idx = lane + 64 i is key idx / (D / 8),
+    // 16-byte chunk idx % (D / 8), so 8 consecutive lanes read one 128-byte line.
+    unsigned koff[VPL], voff[VPL];
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
         const int idx = lane + 64 * i;
+        koff[i] = (unsigned)(idx / (D / 8)) * kts2 + (idx % (D / 8)) * 16;
         voff[i] = (unsigned)(idx / (D / 8)) * vts2 + (idx % (D / 8)) * 16;
     }
 
@@ -185,20 +185,15 @@ __global__ __launch_bounds__(kThreads) void decode_splitk_kernel(DecodeArgs a) {
     float m_i = kNegFloor, l_i = 0.f;
 
     struct TileRegs {
-        s16x8 k[2][KD];
+        s16x8 k[VPL];
         s16x8 v[VPL];
     };
     auto load_tile = [&](int t0, TileRegs& tr) {
         const unsigned kt = t0 < k1 ? (unsigned)t0 * kts2 : kSkip;
         const unsigned vt = t0 < k1 ? (unsigned)t0 * vts2 : kSkip;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int kk = 0; kk < KD; ++kk) {
-                s16x8 v = __builtin_bit_cast(s16x8, __builtin_amdgcn_raw_buffer_load_b128(krs, koff[kb][kk] + kt, 0, kStream));
-                if (32 * kk + 8 * G >= D) v = s16x8{0, 0, 0, 0, 0, 0, 0, 0};  // D = 16 pads d to 32
-                tr.k[kb][kk] = v;
-            }
+        for (int i = 0; i < VPL; ++i)
+            tr.k[i] = __builtin_bit_cast(s16x8, __builtin_amdgcn_raw_buffer_load_b128(krs, koff[i] + kt, 0, kStream));
 #pragma unroll
         for (int i = 0; i < VPL; ++i)
             tr.v[i] = __builtin_bit_cast(s16x8, __builtin_amdgcn_raw_buffer_load_b128(vrs, voff[i] + vt, 0, kStream));
@@ -207,21 +202,31 @@ __global__ __launch_bounds__(kThreads) void decode_splitk_kernel(DecodeArgs a) {
         __builtin_amdgcn_sched_barrier(0);
     };
     auto compute_tile = [&](int t0, const TileRegs& tr, int parity) {
-        // Stage V in this wave's LDS (swizzled, double-buffered) for the transpose read.
-        uint16_t* vs = vlds[wave][parity];
+        // Stage K and V in this wave's LDS (swizzled rows) for the operand reads.
+        uint16_t* ks = klds[wave][parity % NPAR];
+        uint16_t* vs = vlds[wave][parity % NPAR];
 #pragma unroll
         for (int i = 0; i < VPL; ++i) {
             const int idx = lane + 64 * i;
             const int r = idx / (D / 8), ch = idx % (D / 8);
+            *reinterpret_cast<s16x8*>(ks + r * D + ((ch ^ lds_swz<D>(r)) << 3)) = tr.k[i];
             *reinterpret_cast<s16x8*>(vs + r * D + ((ch ^ lds_swz<D>(r)) << 3)) = tr.v[i];
         }
-        // S^T = K Q^T for the two 16-key blocks of the tile.
+        // S^T = K Q^T for the two 16-key blocks of the tile. Row rho of block kb is key
+        // 8 (rho / 4) + 4 kb + rho % 4 (the order of the score registers); lane (rho, G) reads
+        // d = 32 kk + 8 G .. + 7 of it (D = 16 pads d to 32 with zeros).
         f32x4 st[2];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
             st[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+            const int key = 8 * (l16 >> 2) + 4 * kb + (l16 & 3);
 #pragma unroll
-            for (int kk = 0; kk < KD; ++kk) st[kb] = T::mfma16(tr.k[kb][kk], qop[kk], st[kb]);
+            for (int kk = 0; kk < KD; ++kk) {
+                const int d0 = 32 * kk + 8 * G;
+                s16x8 kop = {0, 0, 0, 0, 0, 0, 0, 0};
+                if (d0 < D) kop = *reinterpret_cast<const s16x8*>(ks + lds_off<D>(key, d0));
+                st[kb] = T::mfma16(kop, qop[kk], st[kb]);
+            }
         }
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) st[kb] *= a.qk_scale;
@@ -314,15 +319,66 @@ __global__ __launch_bounds__(kThreads) void decode_splitk_kernel(DecodeArgs a) {
     }
 }
 
-// One wave per output row (batch, head, query): combines the splits that hold visible keys,
-// lse = log2(sum_s 2^lse_s), O = sum_s 2^(lse_s - lse) O_s. Every split's lse is loaded at once
-// (lane = split) and reduced across the wave; the partial O rows are then read as float4,
-// LPS lanes per split row and 64 / LPS split rows per load, four loads in flight per lane.
+// Merge of one output row (batch, head, query) from the n split partials [s_lo, s_lo + n):
+// lse = log2(sum_s 2^lse_s), O = sum_s 2^(lse_s - lse) O_s. The splits go in chunks of up to
+// 64 (lane = split for the lse values; LPS lanes per partial O row, float4 each), and every
+// load of a chunk is issued before the first is used, so a row costs one memory round trip
+// per chunk; chunks after the first rescale the running sums to the new maximum.
+template <int D, typename T>
+__device__ inline void merge_row(const DecodeArgs& a, int64_t rowid, int b, int hh, int qq, int s_lo, int n, int lane) {
+    constexpr int LPS = D / 4;                          // lanes per split row (float4 each)
+    constexpr int SPI = 64 / LPS;                       // split rows per wave-wide load
+    constexpr int CH = SPI * 16 < 64 ? SPI * 16 : 64;   // splits per chunk (<= 16 loads per lane)
+    constexpr int NL = CH / SPI;
+    const __amdgpu_buffer_rsrc_t lrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(a.ws_lse + rowid * a.splits + s_lo), (short)0, n * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(a.ws_o + (rowid * a.splits + s_lo) * D), (short)0, n * D * 4, 0x00020000);
+    const int sub = lane / LPS, d0 = (lane % LPS) * 4;
+    float M = -INFINITY, lsum = 0.f;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int c0 = 0; c0 < n; c0 += CH) {
+        const int cnt = n - c0 < CH ? n - c0 : CH;
+        float ls = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(lrs, (c0 + lane) * 4, 0, 0));
+        f32x4 ov[NL];
+#pragma unroll
+        for (int u = 0; u < NL; ++u)
+            ov[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                ors, ((c0 + u * SPI + sub) * D + d0) * 4, 0, 0));
+        ls = lane < cnt ? ls : -INFINITY;
+        float mc = ls;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) mc = fmaxf(mc, __shfl_xor(mc, off));
+        const float m_new = fmaxf(M, mc);
+        if (m_new == -INFINITY) continue;
+        const float sc = fast_exp2(M - m_new);
+        const float w = fast_exp2(ls - m_new);
+        float ws = w;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) ws += __shfl_xor(ws, off);
+        lsum = lsum * sc + ws;
+        acc *= sc;
+#pragma unroll
+        for (int u = 0; u < NL; ++u) acc += __shfl(w, u * SPI + sub) * ov[u];
+        M = m_new;
+    }
+#pragma unroll
+    for (int off = LPS; off < 64; off <<= 1)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[c] += __shfl_xor(acc[c], off);
+    const bool empty = M == -INFINITY;
+    const float inv = empty ? 0.f : 1.f / lsum;
+    if (lane < LPS) {
+        uint16_t* out = a.o + (int64_t)b * a.obs + (int64_t)qq * a.ots + (int64_t)hh * a.ohs + lane * 4;
+        u32x2 wv = {T::pack2(acc[0] * inv, acc[1] * inv), T::pack2(acc[2] * inv, acc[3] * inv)};
+        *reinterpret_cast<u32x2*>(out) = wv;
+    }
+    if (lane == 0) a.lse[(int64_t)hh * a.lse_hs + (int64_t)b * a.nq + qq] = empty ? INFINITY : M + fast_log2(lsum);
+}
+
+// One wave per output row.
 template <int D, typename T>
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
-    constexpr int LPS = D / 4;       // lanes per split row (float4 each)
-    constexpr int SPI = 64 / LPS;    // split rows per wave-wide load
-    constexpr int UNROLL = 4;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int64_t rowid = (int64_t)blockIdx.x * 4 + wave;  // over batch * num_heads * nq
     const int64_t total = (int64_t)a.batch * a.num_heads * a.nq;
@@ -335,60 +391,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
     const int s_lo = rg.lo / a.chunk;
     int s_hi = rg.hi > rg.lo ? (rg.hi - 1) / a.chunk + 1 : s_lo;
     if (s_hi > a.splits) s_hi = a.splits;
-    const int n = s_hi - s_lo;
-    const float* lse_row = a.ws_lse + rowid * a.splits + s_lo;
-    const float* o_row = a.ws_o + (rowid * a.splits + s_lo) * D;
-
-    // Max over the splits' lse (empty splits hold -inf).
-    float M = -INFINITY;
-    for (int s0 = 0; s0 < n; s0 += 64) {
-        const float v = s0 + lane < n ? lse_row[s0 + lane] : -INFINITY;
-        M = fmaxf(M, v);
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
-
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    float lsum = 0.f;
-    if (M != -INFINITY) {
-        const int sub = lane / LPS, d0 = (lane % LPS) * 4;
-        for (int s0 = 0; s0 < n; s0 += 64) {
-            // Weights of splits s0 .. s0 + 63, one per lane.
-            const float w_lane = s0 + lane < n ? fast_exp2(lse_row[s0 + lane] - M) : 0.f;
-            lsum += w_lane;
-            const int cnt = n - s0 < 64 ? n - s0 : 64;
-            for (int j = 0; j < cnt; j += SPI * UNROLL) {
-                f32x4 ov[UNROLL];
-                float wv[UNROLL];
-#pragma unroll
-                for (int u = 0; u < UNROLL; ++u) {
-                    const int sl = j + u * SPI + sub;  // split within this chunk of 64
-                    const bool ok = sl < cnt;
-                    wv[u] = __shfl(w_lane, ok ? sl : 0);
-                    ov[u] = ok ? *reinterpret_cast<const f32x4*>(o_row + (int64_t)(s0 + sl) * D + d0)
-                               : f32x4{0.f, 0.f, 0.f, 0.f};
-                    if (!ok) wv[u] = 0.f;
-                }
-#pragma unroll
-                for (int u = 0; u < UNROLL; ++u) acc += wv[u] * ov[u];
-            }
-        }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) lsum += __shfl_xor(lsum, off);
-        // Sum the SPI split groups (lanes d-aligned LPS apart).
-#pragma unroll
-        for (int off = LPS; off < 64; off <<= 1)
-#pragma unroll
-            for (int c = 0; c < 4; ++c) acc[c] += __shfl_xor(acc[c], off);
-    }
-    const bool empty = M == -INFINITY;
-    const float inv = empty ? 0.f : 1.f / lsum;
-    if (lane < LPS) {
-        uint16_t* out = a.o + (int64_t)b * a.obs + (int64_t)qq * a.ots + (int64_t)hh * a.ohs + lane * 4;
-        u32x2 w = {T::pack2(acc[0] * inv, acc[1] * inv), T::pack2(acc[2] * inv, acc[3] * inv)};
-        *reinterpret_cast<u32x2*>(out) = w;
-    }
-    if (lane == 0) a.lse[(int64_t)hh * a.lse_hs + (int64_t)b * a.nq + qq] = empty ? INFINITY : M + fast_log2(lsum);
+    merge_row<D, T>(a, rowid, b, hh, qq, s_lo, s_hi - s_lo, lane);
 }
 
 DecodeArgs make_args(const mykfa_decode_params& p, int splits, void* ws) {

@@ -63,9 +63,11 @@ def test_decode_head_dims(d):
     assert_lse(lse, exp_lse)
 
 
-@pytest.mark.parametrize("splits", [1, 2, 3, 7, 16, 64])
+@pytest.mark.parametrize("splits", [1, 2, 3, 7, 16, 64, 128])
 def test_every_split_count_agrees(splits):
-    """The C ABI with an explicit split count: split-K + merge is independent of the split."""
+    """The C ABI with an explicit split count: split-K + merge is independent of the split.
+    128 splits of 32 keys give rows with up to 125 partials: the merge's 64-split chunks and
+    the rescale between them."""
     _say(f"splits={splits}")
     lens = [1000, 17, 4000, 2500]
     q, kc, vc, _, _, cl = _make(len(lens), 4096, lens, 4, 16, 4, 64, seed=2)
