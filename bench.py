@@ -10,7 +10,12 @@ reference times them (scripts/benchmark_attention.py:31-40): eager public-API ca
 events around the repeats; the host enqueues a step (~160 us) faster than the GPU runs it,
 so the GPU never waits. --graph replays a captured HIP graph instead (ROCm 7 adds ~7 us
 between graph kernel nodes, which back-to-back eager launches do not). Decode steps are
-graph replays, as in the reference's scripts/benchmark_decode.py:149-157. Every timed region
+graph replays, as in the reference's scripts/benchmark_decode.py:122-157, which captures a
+whole model decode step (every layer's attention and the rest) in one graph: here one graph
+holds the attention decode of DECODE_LAYERS layers, each with its own caches, and a layer's
+time is the replay time over DECODE_LAYERS. A graph of a single call is timed as well
+("ms_single_call_graph"): each replay carries ~5 us of fixed cost that a model step pays
+once, not once per layer. Every timed region
 follows the W warmup steps and a further ~0.3 s of untimed steps (settle()), so that the
 GPU's clocks have ramped up: the first ~0.2 s of load runs up to 15% slower.
 FLOPs follow the reference's convention (scripts/benchmark_attention.py:49-50, 86):
@@ -217,34 +222,46 @@ def measure_prefill(w, steps: int, warmup: int, backward: bool, use_graph: bool 
     return ms, flops, kern, algo
 
 
+DECODE_LAYERS = 4
+
+
 def measure_decode(w, steps: int, warmup: int):
-    """flash_attn_with_kvcache (append + split-K decode + merge) captured in a graph; replays
-    rotate over independent cache sets totalling > 2 GB so the 256 MB Infinity Cache cannot
-    hold the working set."""
+    """flash_attn_with_kvcache (append + split-K decode + merge) for DECODE_LAYERS layers, each
+    with its own caches (> 4 GB in all, so the 256 MB Infinity Cache cannot hold them),
+    captured in one graph as a model's decode step is; returns the time per layer, the time of
+    a one-call graph (alternating two layers' caches), per-kernel times and the split count."""
     g0 = torch.Generator(device="cuda").manual_seed(0)
     b = len(w.cache_seqlens)
-    nsets = 2
-    sets = []
-    for _ in range(nsets):
+    layers = []
+    for _ in range(DECODE_LAYERS):
         kc = torch.randn(b, w.capacity, w.kv_heads, w.head_dim, device="cuda", generator=g0).to(torch.bfloat16)
         vc = torch.randn(b, w.capacity, w.kv_heads, w.head_dim, device="cuda", generator=g0).to(torch.bfloat16)
-        sets.append((kc, vc))
-    q = torch.randn(b, w.nq, w.heads, w.head_dim, device="cuda", generator=g0).to(torch.bfloat16)
-    kn = torch.randn(b, w.nq, w.kv_heads, w.head_dim, device="cuda", generator=g0).to(torch.bfloat16)
-    vn = torch.randn(b, w.nq, w.kv_heads, w.head_dim, device="cuda", generator=g0).to(torch.bfloat16)
+        q = torch.randn(b, w.nq, w.heads, w.head_dim, device="cuda", generator=g0).to(torch.bfloat16)
+        kn = torch.randn(b, w.nq, w.kv_heads, w.head_dim, device="cuda", generator=g0).to(torch.bfloat16)
+        vn = torch.randn(b, w.nq, w.kv_heads, w.head_dim, device="cuda", generator=g0).to(torch.bfloat16)
+        layers.append((q, kc, vc, kn, vn))
     lens = torch.tensor(w.cache_seqlens, dtype=torch.int32, device="cuda")
-    graphs = []
-    for kc, vc in sets:
-        def step(kc=kc, vc=vc):
-            return flash_attn_with_kvcache(q, kc, vc, kn, vn, cache_seqlens=lens, causal=True)
-        graphs.append(capture(step, warmup))
+
+    def call(layer):
+        q, kc, vc, kn, vn = layer
+        return flash_attn_with_kvcache(q, kc, vc, kn, vn, cache_seqlens=lens, causal=True)
+
+    def model_step():
+        return [call(layer) for layer in layers]
+
+    g_step = capture(model_step, warmup)
+    ms = time_events(g_step.replay, steps, warmup=1) / DECODE_LAYERS
+    singles = [capture(lambda layer=layer: call(layer), warmup) for layer in layers[:2]]
     it = [0]
 
     def replay():
-        graphs[it[0] % nsets].replay()
+        singles[it[0] % 2].replay()
         it[0] += 1
 
-    ms = time_events(replay, steps * nsets, warmup=nsets)
+    ms_single = time_events(replay, steps * 2, warmup=2)
+    sets = [(kc, vc) for _, kc, vc, _, _ in layers[:2]]
+    q = layers[0][0]
+    nsets = 2
     # Per-kernel durations through the C ABI, alternating the cache sets as above (the lengths
     # already include the appended tokens).
     scale = 1.0 / (w.head_dim ** 0.5)
@@ -260,8 +277,8 @@ def measure_decode(w, steps: int, warmup: int):
     kern = {"decode_splitk": time_events(one("splitk"), steps * nsets, warmup=nsets),
             "decode_merge": time_events(one("merge"), steps * nsets, warmup=nsets)}
     splits = calls[0].dp.num_splits
-    del sets, graphs, calls
-    return ms, kern, splits
+    del sets, g_step, singles, calls, layers
+    return ms, ms_single, kern, splits
 
 
 # --- CPU baseline ---------------------------------------------------------------------------------
@@ -359,8 +376,9 @@ def main():
         out = {}
         for name in ("cfg5", "cfg5_mtp"):
             wk = W[name]
-            m, kk, splits = measure_decode(wk, args.steps, args.warmup)
-            out[name] = {"ms": round(m, 5), "GB/s": round(wk.decode_bytes / (m * 1e-3) / 1e9, 1), "splits": splits,
+            m, m1, kk, splits = measure_decode(wk, args.steps, args.warmup)
+            out[name] = {"ms": round(m, 5), "GB/s": round(wk.decode_bytes / (m * 1e-3) / 1e9, 1),
+                         "ms_single_call_graph": round(m1, 5), "splits": splits,
                          "kernel_ms": {k: round(v, 5) for k, v in kk.items()}}
         print(json.dumps({"decode_only": out}), flush=True)
         return
@@ -388,19 +406,21 @@ def main():
         for name in ("cfg5", "cfg5_mtp"):
             wk = W[name]
             log(f"config {wk.name} decode")
-            m, kk, splits = measure_decode(wk, max(10, args.steps // 2), 3)
+            m, m1, kk, splits = measure_decode(wk, max(10, args.steps // 2), 3)
             gbs = wk.decode_bytes / (m * 1e-3) / 1e9
             # Roofline of the split-K kernel: the step's algorithmic bytes (each K/V byte once per
             # GQA group, q, O, LSE) over its own average duration.
             kgbs = wk.decode_bytes / (kk["decode_splitk"] * 1e-3) / 1e9
             configs[name] = {"workload": wk.name, "ms": round(m, 5), "GB/s": round(gbs, 1),
                              "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "bytes": int(wk.decode_bytes),
+                             "layers_per_graph": DECODE_LAYERS, "ms_single_call_graph": round(m1, 5),
+                             "GB/s_single_call_graph": round(wk.decode_bytes / (m1 * 1e-3) / 1e9, 1),
                              "splits": splits, "kernel_ms": {k: round(v, 5) for k, v in kk.items()},
                              "roofline": {"kernel": "decode_splitk", "bound": "hbm", "achieved": round(kgbs, 1),
                                           "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(kgbs / HBM_PEAK_GBS, 4),
                                           "traffic": profiled_traffic("decode_splitk", "cfg5_decode")
                                           if name == "cfg5" else None}}
-            log(f"  {m * 1e3:.1f} us, {gbs:.0f} GB/s; kernels (ms): " + ", ".join(f"{k}={v:.4f}" for k, v in kk.items()))
+            log(f"  {m * 1e3:.1f} us per layer ({m1 * 1e3:.1f} us as a one-call graph), {gbs:.0f} GB/s; kernels (ms): " + ", ".join(f"{k}={v:.4f}" for k, v in kk.items()))
     cpu = None
     if not (args.quick or args.no_cpu):
         log("cpu baseline")
