@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define MYKFA_ABI_VERSION 3
+#define MYKFA_ABI_VERSION 4
 #define MYKFA_UNBOUNDED (1 << 30) /* flash_attn.py:32 (_UNBOUNDED) */
 
 /* Status codes. */
@@ -147,6 +147,97 @@ typedef struct mykfa_kv_append_params {
     int32_t dtype;
 } mykfa_kv_append_params;
 
+/*
+ * Attention-block prologue: q/k RMSNorm (cast back to the input type) followed by the
+ * interleaved-pair rotary embedding, in one pass over q and k. Replaces, in one launch, the
+ * elementwise chain of Attention.forward (mixers.py:85-89): RMSNorm.forward
+ * (model/layers.py:22-25) under bf16 autocast, `.to(v.dtype)`, then RotaryEmbedding.rotate
+ * (model/layers.py:93-98) in fp32 and the cast back.
+ *   q_in/k_in  (batch, seqlen, H, D) views, e.g. of the fused qkv projection output;
+ *   q_out/k_out written in the input type;
+ *   position_ids int64 (batch, seqlen) (batch stride 0 for an expanded arange); a position
+ *   outside [0, table_rows) reads the nearest table row;
+ *   cos/sin fp32 (table_rows, D): RotaryEmbedding.cos_cached / sin_cached (angles repeated
+ *   per pair, layers.py:80-85); both NULL = no rotation;
+ *   q_weight/k_weight fp32 (D,): the RMSNorm weights; both NULL = no norm.
+ * Rounding points follow the reference under autocast: the norm in fp32, rounded to the
+ * input type; the rotation in fp32 (separate products and sum, no fused multiply-add),
+ * rounded to the input type.
+ */
+typedef struct mykfa_qk_prologue_params {
+    const void* q_in;
+    const void* k_in;
+    void* q_out;
+    void* k_out;
+    int64_t qi_batch_stride, qi_token_stride, qi_head_stride;
+    int64_t ki_batch_stride, ki_token_stride, ki_head_stride;
+    int64_t qo_batch_stride, qo_token_stride, qo_head_stride;
+    int64_t ko_batch_stride, ko_token_stride, ko_head_stride;
+    const int64_t* position_ids;
+    int64_t pos_batch_stride, pos_token_stride;
+    const float* cos;
+    const float* sin;
+    int64_t table_stride; /* elements between table rows (>= head_dim, multiple of 4) */
+    int32_t table_rows;
+    const float* q_weight;
+    const float* k_weight;
+    float eps;
+    int32_t batch;
+    int32_t seqlen;
+    int32_t num_heads;
+    int32_t num_kv_heads;
+    int32_t head_dim;
+    int32_t dtype;
+} mykfa_qk_prologue_params;
+
+/*
+ * Prologue backward: gradients of q_in/k_in from those of q_out/k_out (autograd of the
+ * forward chain above), the RMSNorm weight gradients summed over every token and head in a
+ * fixed order (deterministic), and optionally a copy of the value gradient dv_src into dv_dst
+ * so that one launch fills a whole fused-projection gradient (q | k | v slices).
+ * fwd.q_in/k_in/positions/tables/weights/eps must be those of the forward call; fwd.q_out and
+ * fwd.k_out are ignored. dq_weight/dk_weight (fp32 (D,)) are written, not accumulated, and are
+ * required exactly when the forward had weights.
+ */
+typedef struct mykfa_qk_prologue_bwd_params {
+    mykfa_qk_prologue_params fwd;
+    const void* dq_out;
+    const void* dk_out;
+    void* dq_in;
+    void* dk_in;
+    int64_t dqo_batch_stride, dqo_token_stride, dqo_head_stride;
+    int64_t dko_batch_stride, dko_token_stride, dko_head_stride;
+    int64_t dqi_batch_stride, dqi_token_stride, dqi_head_stride;
+    int64_t dki_batch_stride, dki_token_stride, dki_head_stride;
+    const void* dv_src; /* (batch, seqlen, Hkv, D) or NULL */
+    void* dv_dst;
+    int64_t dvs_batch_stride, dvs_token_stride, dvs_head_stride;
+    int64_t dvd_batch_stride, dvd_token_stride, dvd_head_stride;
+    float* dq_weight;
+    float* dk_weight;
+} mykfa_qk_prologue_bwd_params;
+
+/*
+ * Attention-block epilogue: the output gate y = x * sigmoid(gate) (mixers.py:116-117) over
+ * rows of `width` elements, with the reference's autocast rounding points (sigmoid rounded to
+ * the input type, then the product rounded). Backward: dx = dy * s, and
+ * dgate = (dy * x rounded) * (1 - s) * s, s = the rounded sigmoid (torch's mul and
+ * sigmoid_backward). Row strides in elements; width a multiple of 8.
+ */
+typedef struct mykfa_gate_params {
+    const void* x;
+    const void* gate;
+    void* y;       /* forward output */
+    const void* dy; /* backward inputs/outputs (unused by the forward) */
+    void* dx;
+    void* dgate;
+    int64_t x_row_stride, gate_row_stride, y_row_stride;
+    int64_t dy_row_stride, dx_row_stride, dgate_row_stride;
+    int64_t rows;
+    int32_t width;
+    int32_t dtype;
+} mykfa_gate_params;
+
 /* ---- version / errors ------------------------------------------------------------- */
 int mykfa_abi_version(void);
 const char* mykfa_version(void);
@@ -206,6 +297,26 @@ int mykfa_decode(const mykfa_decode_params* p, void* workspace, size_t workspace
 /* Replaces the advanced-index cache writes of flash_attn_with_kvcache
  * (flash_attn.py:480-485); graph-capturable (no host sync). */
 int mykfa_kv_append(const mykfa_kv_append_params* p, mykfa_stream_t stream);
+
+/* ---- attention-block prologue / epilogue -------------------------------------------- */
+size_t mykfa_sizeof_qk_prologue_params(void);
+size_t mykfa_sizeof_qk_prologue_bwd_params(void);
+size_t mykfa_sizeof_gate_params(void);
+int mykfa_validate_qk_prologue(const mykfa_qk_prologue_params* p);
+int mykfa_validate_qk_prologue_bwd(const mykfa_qk_prologue_bwd_params* p);
+int mykfa_validate_gate(const mykfa_gate_params* p, int backward);
+/* q/k RMSNorm + RoPE (replaces mixers.py:85-89 with layers.py:22-25, :93-98). */
+int mykfa_qk_prologue_fwd(const mykfa_qk_prologue_params* p, mykfa_stream_t stream);
+/* fp32 workspace the backward needs for its weight-gradient partials (0 without norm). */
+size_t mykfa_qk_prologue_bwd_workspace_size(int32_t batch, int32_t seqlen, int32_t num_heads,
+                                            int32_t num_kv_heads, int32_t head_dim);
+/* Gradients of the prologue (autograd of mixers.py:85-89), plus the optional dv copy. */
+int mykfa_qk_prologue_bwd(const mykfa_qk_prologue_bwd_params* p, void* workspace, size_t workspace_bytes,
+                          mykfa_stream_t stream);
+/* y = x * sigmoid(gate) (replaces mixers.py:116-117). */
+int mykfa_gate_fwd(const mykfa_gate_params* p, mykfa_stream_t stream);
+/* dx, dgate from dy (autograd of mixers.py:116-117). */
+int mykfa_gate_bwd(const mykfa_gate_params* p, mykfa_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -12,7 +12,7 @@ import os
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmykfa.so"
-ABI_VERSION = 3  # MYKFA_ABI_VERSION
+ABI_VERSION = 4  # MYKFA_ABI_VERSION
 
 OK = 0
 ERR_INVALID = 1
@@ -74,6 +74,45 @@ class KvAppendParams(ctypes.Structure):
     ]
 
 
+class QkPrologueParams(ctypes.Structure):
+    _fields_ = [
+        ("q_in", _ptr), ("k_in", _ptr), ("q_out", _ptr), ("k_out", _ptr),
+        ("qi_batch_stride", _i64), ("qi_token_stride", _i64), ("qi_head_stride", _i64),
+        ("ki_batch_stride", _i64), ("ki_token_stride", _i64), ("ki_head_stride", _i64),
+        ("qo_batch_stride", _i64), ("qo_token_stride", _i64), ("qo_head_stride", _i64),
+        ("ko_batch_stride", _i64), ("ko_token_stride", _i64), ("ko_head_stride", _i64),
+        ("position_ids", _ptr), ("pos_batch_stride", _i64), ("pos_token_stride", _i64),
+        ("cos", _ptr), ("sin", _ptr), ("table_stride", _i64), ("table_rows", _i32),
+        ("q_weight", _ptr), ("k_weight", _ptr), ("eps", _f32),
+        ("batch", _i32), ("seqlen", _i32), ("num_heads", _i32), ("num_kv_heads", _i32),
+        ("head_dim", _i32), ("dtype", _i32),
+    ]
+
+
+class QkPrologueBwdParams(ctypes.Structure):
+    _fields_ = [
+        ("fwd", QkPrologueParams),
+        ("dq_out", _ptr), ("dk_out", _ptr), ("dq_in", _ptr), ("dk_in", _ptr),
+        ("dqo_batch_stride", _i64), ("dqo_token_stride", _i64), ("dqo_head_stride", _i64),
+        ("dko_batch_stride", _i64), ("dko_token_stride", _i64), ("dko_head_stride", _i64),
+        ("dqi_batch_stride", _i64), ("dqi_token_stride", _i64), ("dqi_head_stride", _i64),
+        ("dki_batch_stride", _i64), ("dki_token_stride", _i64), ("dki_head_stride", _i64),
+        ("dv_src", _ptr), ("dv_dst", _ptr),
+        ("dvs_batch_stride", _i64), ("dvs_token_stride", _i64), ("dvs_head_stride", _i64),
+        ("dvd_batch_stride", _i64), ("dvd_token_stride", _i64), ("dvd_head_stride", _i64),
+        ("dq_weight", _ptr), ("dk_weight", _ptr),
+    ]
+
+
+class GateParams(ctypes.Structure):
+    _fields_ = [
+        ("x", _ptr), ("gate", _ptr), ("y", _ptr), ("dy", _ptr), ("dx", _ptr), ("dgate", _ptr),
+        ("x_row_stride", _i64), ("gate_row_stride", _i64), ("y_row_stride", _i64),
+        ("dy_row_stride", _i64), ("dx_row_stride", _i64), ("dgate_row_stride", _i64),
+        ("rows", _i64), ("width", _i32), ("dtype", _i32),
+    ]
+
+
 # Every symbol include/mykfa.h declares, with (restype, argtypes).
 SIGNATURES = {
     "mykfa_abi_version": (ctypes.c_int, []),
@@ -98,6 +137,17 @@ SIGNATURES = {
     "mykfa_decode_merge": (ctypes.c_int, [ctypes.POINTER(DecodeParams), _ptr, ctypes.c_size_t, _ptr]),
     "mykfa_decode": (ctypes.c_int, [ctypes.POINTER(DecodeParams), _ptr, ctypes.c_size_t, _ptr]),
     "mykfa_kv_append": (ctypes.c_int, [ctypes.POINTER(KvAppendParams), _ptr]),
+    "mykfa_sizeof_qk_prologue_params": (ctypes.c_size_t, []),
+    "mykfa_sizeof_qk_prologue_bwd_params": (ctypes.c_size_t, []),
+    "mykfa_sizeof_gate_params": (ctypes.c_size_t, []),
+    "mykfa_validate_qk_prologue": (ctypes.c_int, [ctypes.POINTER(QkPrologueParams)]),
+    "mykfa_validate_qk_prologue_bwd": (ctypes.c_int, [ctypes.POINTER(QkPrologueBwdParams)]),
+    "mykfa_validate_gate": (ctypes.c_int, [ctypes.POINTER(GateParams), ctypes.c_int]),
+    "mykfa_qk_prologue_fwd": (ctypes.c_int, [ctypes.POINTER(QkPrologueParams), _ptr]),
+    "mykfa_qk_prologue_bwd_workspace_size": (ctypes.c_size_t, [_i32, _i32, _i32, _i32, _i32]),
+    "mykfa_qk_prologue_bwd": (ctypes.c_int, [ctypes.POINTER(QkPrologueBwdParams), _ptr, ctypes.c_size_t, _ptr]),
+    "mykfa_gate_fwd": (ctypes.c_int, [ctypes.POINTER(GateParams), _ptr]),
+    "mykfa_gate_bwd": (ctypes.c_int, [ctypes.POINTER(GateParams), _ptr]),
 }
 
 _STRUCT_SIZES = {
@@ -105,6 +155,9 @@ _STRUCT_SIZES = {
     "mykfa_sizeof_bwd_params": BwdParams,
     "mykfa_sizeof_decode_params": DecodeParams,
     "mykfa_sizeof_kv_append_params": KvAppendParams,
+    "mykfa_sizeof_qk_prologue_params": QkPrologueParams,
+    "mykfa_sizeof_qk_prologue_bwd_params": QkPrologueBwdParams,
+    "mykfa_sizeof_gate_params": GateParams,
 }
 
 _lib: ctypes.CDLL | None = None

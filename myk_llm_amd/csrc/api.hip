@@ -161,6 +161,108 @@ int check_append(const mykfa_kv_append_params* p) {
     return ok();
 }
 
+// A (batch, token, head) view read or written 16 bytes at a time by the elementwise kernels
+// (64-bit addressing: no span limit).
+int check_view(const void* ptr, int64_t bs, int64_t ts, int64_t hs, const char* name) {
+    if (ptr == nullptr) return fail(MYKFA_ERR_INVALID, "%s is NULL", name);
+    if (!aligned16(ptr)) return fail(MYKFA_ERR_INVALID, "%s must be 16-byte aligned", name);
+    if (!stride_ok(bs) || !stride_ok(ts) || !stride_ok(hs))
+        return fail(MYKFA_ERR_INVALID, "%s strides (%lld, %lld, %lld) must be non-negative multiples of 8 elements",
+                    name, (long long)bs, (long long)ts, (long long)hs);
+    return MYKFA_OK;
+}
+
+// mixers.py:85-89 with RMSNorm (layers.py:15-25) and RotaryEmbedding (layers.py:73-101).
+// `outputs`: whether q_out/k_out are written (the backward ignores them).
+int check_prologue(const mykfa_qk_prologue_params* p, bool outputs = true) {
+    if (p == nullptr) return fail(MYKFA_ERR_INVALID, "params is NULL");
+    if (p->dtype != MYKFA_BF16 && p->dtype != MYKFA_FP16)
+        return fail(MYKFA_ERR_UNSUPPORTED, "the q/k prologue needs bf16/fp16 q, k; got dtype code %d", p->dtype);
+    if (!head_dim_supported(p->head_dim))
+        return fail(MYKFA_ERR_UNSUPPORTED, "head_dim must be one of [16, 32, 64, 128, 256]; got %d", p->head_dim);
+    if (p->batch < 0 || p->seqlen < 0 || p->num_heads < 0 || p->num_kv_heads < 0)
+        return fail(MYKFA_ERR_INVALID, "negative shape (batch %d, seqlen %d, heads %d, kv heads %d)", p->batch,
+                    p->seqlen, p->num_heads, p->num_kv_heads);
+    if ((p->q_weight == nullptr) != (p->k_weight == nullptr))
+        return fail(MYKFA_ERR_INVALID, "q_weight and k_weight must both be given or both be NULL");
+    if ((p->cos == nullptr) != (p->sin == nullptr))
+        return fail(MYKFA_ERR_INVALID, "cos and sin must both be given or both be NULL");
+    const bool work = p->batch > 0 && p->seqlen > 0 && p->num_heads + p->num_kv_heads > 0;
+    if (!work) return MYKFA_OK;
+    int rc;
+    if (p->num_heads > 0) {
+        if ((rc = check_view(p->q_in, p->qi_batch_stride, p->qi_token_stride, p->qi_head_stride, "q_in"))) return rc;
+        if (outputs && (rc = check_view(p->q_out, p->qo_batch_stride, p->qo_token_stride, p->qo_head_stride, "q_out"))) return rc;
+    }
+    if (p->num_kv_heads > 0) {
+        if ((rc = check_view(p->k_in, p->ki_batch_stride, p->ki_token_stride, p->ki_head_stride, "k_in"))) return rc;
+        if (outputs && (rc = check_view(p->k_out, p->ko_batch_stride, p->ko_token_stride, p->ko_head_stride, "k_out"))) return rc;
+    }
+    if (p->q_weight != nullptr) {
+        if (!aligned16(p->q_weight) || !aligned16(p->k_weight))
+            return fail(MYKFA_ERR_INVALID, "q_weight and k_weight must be 16-byte aligned");
+        if (!(p->eps >= 0.0f) || p->eps > 1e30f) return fail(MYKFA_ERR_INVALID, "eps must be finite and >= 0");
+    }
+    if (p->cos != nullptr) {
+        if (p->position_ids == nullptr) return fail(MYKFA_ERR_INVALID, "position_ids is NULL");
+        if ((reinterpret_cast<uintptr_t>(p->position_ids) & 7) != 0)
+            return fail(MYKFA_ERR_INVALID, "position_ids must be 8-byte aligned int64");
+        if (p->pos_batch_stride < 0 || p->pos_token_stride < 0)
+            return fail(MYKFA_ERR_INVALID, "position_ids strides must be non-negative");
+        if (!aligned16(p->cos) || !aligned16(p->sin))
+            return fail(MYKFA_ERR_INVALID, "cos and sin tables must be 16-byte aligned");
+        if (p->table_rows <= 0) return fail(MYKFA_ERR_INVALID, "table_rows must be positive; got %d", p->table_rows);
+        if (p->table_stride < p->head_dim || (p->table_stride & 3) != 0)
+            return fail(MYKFA_ERR_INVALID, "table_stride %lld must be >= head_dim and a multiple of 4",
+                        (long long)p->table_stride);
+    }
+    return MYKFA_OK;
+}
+
+int check_prologue_bwd(const mykfa_qk_prologue_bwd_params* p) {
+    if (p == nullptr) return fail(MYKFA_ERR_INVALID, "params is NULL");
+    int rc = check_prologue(&p->fwd, false);
+    if (rc) return rc;
+    const mykfa_qk_prologue_params& f = p->fwd;
+    if ((p->dv_src == nullptr) != (p->dv_dst == nullptr))
+        return fail(MYKFA_ERR_INVALID, "dv_src and dv_dst must both be given or both be NULL");
+    if (f.q_weight != nullptr && (p->dq_weight == nullptr || p->dk_weight == nullptr))
+        return fail(MYKFA_ERR_INVALID, "dq_weight and dk_weight are required when the forward had weights");
+    const bool work = f.batch > 0 && f.seqlen > 0;
+    if (!work) return MYKFA_OK;
+    if (f.num_heads > 0) {
+        if ((rc = check_view(p->dq_out, p->dqo_batch_stride, p->dqo_token_stride, p->dqo_head_stride, "dq_out"))) return rc;
+        if ((rc = check_view(p->dq_in, p->dqi_batch_stride, p->dqi_token_stride, p->dqi_head_stride, "dq_in"))) return rc;
+    }
+    if (f.num_kv_heads > 0) {
+        if ((rc = check_view(p->dk_out, p->dko_batch_stride, p->dko_token_stride, p->dko_head_stride, "dk_out"))) return rc;
+        if ((rc = check_view(p->dk_in, p->dki_batch_stride, p->dki_token_stride, p->dki_head_stride, "dk_in"))) return rc;
+        if (p->dv_src != nullptr) {
+            if ((rc = check_view(p->dv_src, p->dvs_batch_stride, p->dvs_token_stride, p->dvs_head_stride, "dv_src"))) return rc;
+            if ((rc = check_view(p->dv_dst, p->dvd_batch_stride, p->dvd_token_stride, p->dvd_head_stride, "dv_dst"))) return rc;
+        }
+    }
+    return MYKFA_OK;
+}
+
+// mixers.py:116-117.
+int check_gate(const mykfa_gate_params* p, bool backward) {
+    if (p == nullptr) return fail(MYKFA_ERR_INVALID, "params is NULL");
+    if (p->dtype != MYKFA_BF16 && p->dtype != MYKFA_FP16)
+        return fail(MYKFA_ERR_UNSUPPORTED, "the output gate needs bf16/fp16 tensors; got dtype code %d", p->dtype);
+    if (p->rows < 0 || p->width <= 0 || (p->width & 7) != 0)
+        return fail(MYKFA_ERR_INVALID, "rows (%lld) must be >= 0 and width (%d) a positive multiple of 8",
+                    (long long)p->rows, p->width);
+    if (p->rows == 0) return MYKFA_OK;
+    int rc;
+    if ((rc = check_view(p->x, 0, p->x_row_stride, 0, "x"))) return rc;
+    if ((rc = check_view(p->gate, 0, p->gate_row_stride, 0, "gate"))) return rc;
+    if (!backward) return check_view(p->y, 0, p->y_row_stride, 0, "y");
+    if ((rc = check_view(p->dy, 0, p->dy_row_stride, 0, "dy"))) return rc;
+    if ((rc = check_view(p->dx, 0, p->dx_row_stride, 0, "dx"))) return rc;
+    return check_view(p->dgate, 0, p->dgate_row_stride, 0, "dgate");
+}
+
 hipStream_t as_stream(mykfa_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
 int choose_splits(const mykfa_decode_params* p) {
@@ -271,6 +373,70 @@ int mykfa_kv_append(const mykfa_kv_append_params* p, mykfa_stream_t stream) {
     if (rc) return rc;
     if (p->batch == 0 || p->seqlen_new == 0) return ok();
     return launched(mykfa::launch_kv_append(*p, as_stream(stream)), "mykfa_kv_append");
+}
+
+size_t mykfa_sizeof_qk_prologue_params(void) { return sizeof(mykfa_qk_prologue_params); }
+size_t mykfa_sizeof_qk_prologue_bwd_params(void) { return sizeof(mykfa_qk_prologue_bwd_params); }
+size_t mykfa_sizeof_gate_params(void) { return sizeof(mykfa_gate_params); }
+
+int mykfa_validate_qk_prologue(const mykfa_qk_prologue_params* p) {
+    int rc = check_prologue(p);
+    return rc ? rc : ok();
+}
+int mykfa_validate_qk_prologue_bwd(const mykfa_qk_prologue_bwd_params* p) {
+    int rc = check_prologue_bwd(p);
+    return rc ? rc : ok();
+}
+int mykfa_validate_gate(const mykfa_gate_params* p, int backward) {
+    int rc = check_gate(p, backward != 0);
+    return rc ? rc : ok();
+}
+
+int mykfa_qk_prologue_fwd(const mykfa_qk_prologue_params* p, mykfa_stream_t stream) {
+    int rc = check_prologue(p);
+    if (rc) return rc;
+    if ((long long)p->batch * p->seqlen * (p->num_heads + p->num_kv_heads) == 0) return ok();
+    return launched(mykfa::launch_qk_prologue_fwd(*p, as_stream(stream)), "mykfa_qk_prologue_fwd");
+}
+
+size_t mykfa_qk_prologue_bwd_workspace_size(int32_t batch, int32_t seqlen, int32_t num_heads, int32_t num_kv_heads,
+                                            int32_t head_dim) {
+    if (batch < 0 || seqlen < 0 || num_heads < 0 || num_kv_heads < 0 || !head_dim_supported(head_dim)) return 0;
+    return mykfa::qk_prologue_bwd_workspace_bytes(batch, seqlen, num_heads, num_kv_heads, head_dim);
+}
+
+int mykfa_qk_prologue_bwd(const mykfa_qk_prologue_bwd_params* p, void* workspace, size_t workspace_bytes,
+                          mykfa_stream_t stream) {
+    int rc = check_prologue_bwd(p);
+    if (rc) return rc;
+    const mykfa_qk_prologue_params& f = p->fwd;
+    // With no rows and no norm there is nothing to write; with a norm the launch still writes
+    // the (zero) weight gradients.
+    if ((long long)f.batch * f.seqlen * (f.num_heads + f.num_kv_heads) == 0 && f.q_weight == nullptr) return ok();
+    if (f.q_weight != nullptr) {
+        const size_t need = (size_t)mykfa::qk_prologue_bwd_blocks(f.batch, f.seqlen, f.num_heads, f.num_kv_heads,
+                                                                  f.head_dim) *
+                            2 * f.head_dim * sizeof(float);
+        if (workspace == nullptr || workspace_bytes < need)
+            return fail(MYKFA_ERR_WORKSPACE, "prologue backward workspace needs %zu bytes; got %zu", need,
+                        workspace_bytes);
+        if (!aligned16(workspace)) return fail(MYKFA_ERR_INVALID, "workspace must be 16-byte aligned");
+    }
+    return launched(mykfa::launch_qk_prologue_bwd(*p, workspace, as_stream(stream)), "mykfa_qk_prologue_bwd");
+}
+
+int mykfa_gate_fwd(const mykfa_gate_params* p, mykfa_stream_t stream) {
+    int rc = check_gate(p, false);
+    if (rc) return rc;
+    if (p->rows == 0) return ok();
+    return launched(mykfa::launch_gate(*p, false, as_stream(stream)), "mykfa_gate_fwd");
+}
+
+int mykfa_gate_bwd(const mykfa_gate_params* p, mykfa_stream_t stream) {
+    int rc = check_gate(p, true);
+    if (rc) return rc;
+    if (p->rows == 0) return ok();
+    return launched(mykfa::launch_gate(*p, true, as_stream(stream)), "mykfa_gate_bwd");
 }
 
 }  // extern "C"

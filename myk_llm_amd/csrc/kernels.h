@@ -24,4 +24,13 @@ hipError_t launch_decode_merge(const mykfa_decode_params& p, int num_splits, con
 
 hipError_t launch_kv_append(const mykfa_kv_append_params& p, hipStream_t stream);
 
+// Attention-block prologue (q/k RMSNorm + RoPE) and epilogue (output gate), block_io.hip.
+// The backward's grid (bounded, so the weight-gradient partials have a fixed count) and the
+// fp32 workspace holding one (2, head_dim) partial per workgroup.
+int qk_prologue_bwd_blocks(int batch, int seqlen, int num_heads, int num_kv_heads, int head_dim);
+size_t qk_prologue_bwd_workspace_bytes(int batch, int seqlen, int num_heads, int num_kv_heads, int head_dim);
+hipError_t launch_qk_prologue_fwd(const mykfa_qk_prologue_params& p, hipStream_t stream);
+hipError_t launch_qk_prologue_bwd(const mykfa_qk_prologue_bwd_params& p, void* ws, hipStream_t stream);
+hipError_t launch_gate(const mykfa_gate_params& p, bool backward, hipStream_t stream);
+
 }  // namespace mykfa
