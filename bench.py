@@ -281,6 +281,130 @@ def measure_decode(w, steps: int, warmup: int):
     return ms, ms_single, kern, splits
 
 
+def measure_block_io(w, steps: int):
+    """The attention block's prologue (q/k RMSNorm + RoPE on the fused projection, forward and
+    backward with the value-gradient copy) and epilogue (output gate, forward and backward) at
+    workload w's shape (positions restart at every document), as direct C-ABI launches on
+    prepared buffers. Algorithmic bytes: every tensor element read or written once, plus each
+    distinct cos/sin table row once. Beside them, the reference's composed PyTorch chain
+    (mixers.py:85-89, :116-117 under autocast: separate elementwise kernels) on the same GPU."""
+    from myk_llm_amd import block_io as bio
+
+    t, hq, hkv, d = sum(w.lengths), w.heads, w.kv_heads, w.head_dim
+    g = torch.Generator(device="cuda").manual_seed(1)
+    qkv = torch.randn(t, (hq + 2 * hkv) * d, device="cuda", generator=g).to(torch.bfloat16)
+    pos = torch.cat([torch.arange(n, device="cuda") for n in w.lengths])
+    table_rows = max(w.lengths)
+    cos, sin = bio.rope_tables(d, table_rows, 500000.0, device="cuda")
+    qw = 1 + 0.1 * torch.randn(d, device="cuda", generator=g)
+    kw = 1 + 0.1 * torch.randn(d, device="cuda", generator=g)
+    dq = torch.randn(t, hq, d, device="cuda", generator=g).to(torch.bfloat16)
+    dk = torch.randn(t, hkv, d, device="cuda", generator=g).to(torch.bfloat16)
+    dv = torch.randn(t, hkv, d, device="cuda", generator=g).to(torch.bfloat16)
+    L = _lib.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    x = qkv.unsqueeze(0)
+    q_in = x[..., :hq * d].view(1, t, hq, d)
+    k_in = x[..., hq * d:(hq + hkv) * d].view(1, t, hkv, d)
+    q_out, k_out = torch.empty_like(q_in, memory_format=torch.contiguous_format), torch.empty(1, t, hkv, d, dtype=qkv.dtype, device="cuda")
+    pos2 = pos.unsqueeze(0)
+    fp = bio._prologue_params(q_in, k_in, q_out, k_out, pos2, cos, sin, qw, kw, 1e-6)
+    dqkv = torch.empty_like(x)
+    bp = _lib.QkPrologueBwdParams()
+    bp.fwd = fp
+    dq4, dk4, dv4 = dq.unsqueeze(0), dk.unsqueeze(0), dv.unsqueeze(0)
+    dq_in = dqkv[..., :hq * d].view(1, t, hq, d)
+    dk_in = dqkv[..., hq * d:(hq + hkv) * d].view(1, t, hkv, d)
+    dv_dst = dqkv[..., (hq + hkv) * d:].view(1, t, hkv, d)
+    bp.dq_out, bp.dk_out, bp.dq_in, bp.dk_in = dq4.data_ptr(), dk4.data_ptr(), dq_in.data_ptr(), dk_in.data_ptr()
+    bp.dqo_batch_stride, bp.dqo_token_stride, bp.dqo_head_stride = bio._strides3(dq4)
+    bp.dko_batch_stride, bp.dko_token_stride, bp.dko_head_stride = bio._strides3(dk4)
+    bp.dqi_batch_stride, bp.dqi_token_stride, bp.dqi_head_stride = bio._strides3(dq_in)
+    bp.dki_batch_stride, bp.dki_token_stride, bp.dki_head_stride = bio._strides3(dk_in)
+    bp.dv_src, bp.dv_dst = dv4.data_ptr(), dv_dst.data_ptr()
+    bp.dvs_batch_stride, bp.dvs_token_stride, bp.dvs_head_stride = bio._strides3(dv4)
+    bp.dvd_batch_stride, bp.dvd_token_stride, bp.dvd_head_stride = bio._strides3(dv_dst)
+    dqw, dkw = torch.empty(d, device="cuda"), torch.empty(d, device="cuda")
+    bp.dq_weight, bp.dk_weight = dqw.data_ptr(), dkw.data_ptr()
+    nws = L.mykfa_qk_prologue_bwd_workspace_size(1, t, hq, hkv, d)
+    ws = torch.empty(nws, dtype=torch.uint8, device="cuda")
+
+    width = hq * d
+    og = torch.randn(t, width, device="cuda", generator=g).to(torch.bfloat16)
+    gg = torch.randn(t, width, device="cuda", generator=g).to(torch.bfloat16)
+    dy = torch.randn(t, width, device="cuda", generator=g).to(torch.bfloat16)
+    y, dx, dg = torch.empty_like(og), torch.empty_like(og), torch.empty_like(og)
+    gp = bio._gate_params(og, gg, y, dy, dx, dg)
+
+    calls = {
+        "prologue_fwd": lambda: _lib.check(L.mykfa_qk_prologue_fwd(ctypes.byref(fp), stream)),
+        "prologue_bwd": lambda: _lib.check(L.mykfa_qk_prologue_bwd(ctypes.byref(bp), ws.data_ptr(), nws, stream)),
+        "gate_fwd": lambda: _lib.check(L.mykfa_gate_fwd(ctypes.byref(gp), stream)),
+        "gate_bwd": lambda: _lib.check(L.mykfa_gate_bwd(ctypes.byref(gp), stream)),
+    }
+    e = 2  # bytes per element
+    qk = t * (hq + hkv) * d * e
+    tables = 2 * table_rows * d * 4
+    algo = {
+        "prologue_fwd": 2 * qk + t * 8 + tables + 2 * d * 4,
+        "prologue_bwd": 3 * qk + 2 * t * hkv * d * e + t * 8 + tables + 4 * d * 4,
+        "gate_fwd": 3 * t * width * e,
+        "gate_bwd": 5 * t * width * e,
+    }
+    out = {}
+    reps = max(steps, 20)
+    for name, fn in calls.items():
+        ms = time_events(fn, reps)
+        gbs = algo[name] / (ms * 1e-3) / 1e9
+        out[name] = {"us": round(ms * 1e3, 2), "bytes": int(algo[name]), "GB/s": round(gbs, 1),
+                     "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+
+    # The reference's chain on the same GPU, forward and forward + backward (autocast rounding
+    # points written out: fp32 norm, cast, fp32 rotation, cast; bf16 sigmoid, bf16 product).
+    cos_t, sin_t = cos, sin
+
+    def rot_half(u):
+        return torch.stack((-u[..., 1::2], u[..., ::2]), dim=-1).flatten(start_dim=-2)
+
+    def torch_prologue(xq, xk, wq, wk):
+        def norm(u, wt):
+            u32 = u.float()
+            return (u32 * torch.rsqrt(u32.pow(2).mean(-1, keepdim=True) + 1e-6) * wt).to(u.dtype)
+
+        c, s_ = cos_t[pos2].unsqueeze(2), sin_t[pos2].unsqueeze(2)
+
+        def rope(u):
+            u32 = u.float()
+            return (u32 * c + rot_half(u32) * s_).to(u.dtype)
+
+        return rope(norm(xq, wq)), rope(norm(xk, wk))
+
+    xr = x.detach().requires_grad_(True)
+    wq_r, wk_r = qw.clone().requires_grad_(True), kw.clone().requires_grad_(True)
+
+    def torch_fwd():
+        return torch_prologue(xr[..., :hq * d].view(1, t, hq, d), xr[..., hq * d:(hq + hkv) * d].view(1, t, hkv, d),
+                              wq_r, wk_r)
+
+    def torch_fwdbwd():
+        a, b = torch_fwd()
+        return torch.autograd.grad((a, b, xr[..., (hq + hkv) * d:].view(1, t, hkv, d)), (xr, wq_r, wk_r),
+                                   (dq4, dk4, dv4))
+
+    ogr, ggr = og.detach().requires_grad_(True), gg.detach().requires_grad_(True)
+
+    def torch_gate_fwdbwd():
+        yy = ogr * torch.sigmoid(ggr)
+        return torch.autograd.grad(yy, (ogr, ggr), dy)
+
+    out["torch_chain_us"] = {"prologue_fwd": round(time_events(torch_fwd, 20) * 1e3, 1),
+                             "prologue_fwd+bwd": round(time_events(torch_fwdbwd, 20) * 1e3, 1),
+                             "gate_fwd": round(time_events(lambda: og * torch.sigmoid(gg), 20) * 1e3, 1),
+                             "gate_fwd+bwd": round(time_events(torch_gate_fwdbwd, 20) * 1e3, 1)}
+    out["shape"] = {"tokens": t, "heads": hq, "kv_heads": hkv, "head_dim": d, "gate_width": width}
+    return out
+
+
 # --- CPU baseline ---------------------------------------------------------------------------------
 
 
@@ -350,6 +474,8 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only: no other configs, no CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-only", action="store_true", help="only the decode configs (for profiling)")
+    ap.add_argument("--block-io-only", action="store_true",
+                    help="only the attention-block prologue / epilogue kernels at the cfg3 shape (for profiling)")
     ap.add_argument("--graph", action="store_true", help="time prefill steps as HIP graph replays instead of eager calls")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run a plain 256 MiB fp32 copy kernel 3 times (reads and writes 2^28 bytes "
@@ -381,6 +507,9 @@ def main():
                          "ms_single_call_graph": round(m1, 5), "splits": splits,
                          "kernel_ms": {k: round(v, 5) for k, v in kk.items()}}
         print(json.dumps({"decode_only": out}), flush=True)
+        return
+    if args.block_io_only:
+        print(json.dumps({"block_io_cfg3": measure_block_io(W["cfg3"], args.steps)}), flush=True)
         return
     w = W[args.workload]
     log(f"headline {w.name}: fwd+bwd, steps={args.steps} warmup={args.warmup}")
@@ -421,6 +550,9 @@ def main():
                                           "traffic": profiled_traffic("decode_splitk", "cfg5_decode")
                                           if name == "cfg5" else None}}
             log(f"  {m * 1e3:.1f} us per layer ({m1 * 1e3:.1f} us as a one-call graph), {gbs:.0f} GB/s; kernels (ms): " + ", ".join(f"{k}={v:.4f}" for k, v in kk.items()))
+        log("attention-block prologue / epilogue at the cfg3 shape")
+        configs["block_io_cfg3"] = measure_block_io(W["cfg3"], args.steps)
+        log("  " + json.dumps(configs["block_io_cfg3"]))
     cpu = None
     if not (args.quick or args.no_cpu):
         log("cpu baseline")

@@ -24,6 +24,7 @@ import torch.nn.functional as F
 
 from _util import assert_close
 from myk_llm_amd import flash_attn_func, flash_attn_varlen_func, flash_attn_with_kvcache
+from myk_llm_amd.block_io import output_gate, qkv_norm_rope, rope_tables
 from oracle.attention import reference, reference_varlen
 
 pytestmark = pytest.mark.gpu
@@ -61,7 +62,7 @@ def _linear(x, w):
 class Block:
     """One attention block; `attend(q, k, v)` is supplied per pass (full, cached, packed)."""
 
-    def __init__(self, gen, local):
+    def __init__(self, gen, local, fused=False):
         def p(*shape, scale=0.08):
             return (torch.randn(*shape, generator=gen) * scale).to(torch.bfloat16).cuda()
 
@@ -73,9 +74,18 @@ class Block:
         self.w_gate = p(HEADS * HEAD_DIM, HIDDEN)
         self.qn = (1.0 + 0.1 * torch.randn(HEAD_DIM, generator=gen)).cuda()
         self.kn = (1.0 + 0.1 * torch.randn(HEAD_DIM, generator=gen)).cuda()
+        # fused: the prologue / epilogue kernels (myk_llm_amd.block_io) instead of torch ops
+        self.fused = fused
+        self.cos, self.sin = rope_tables(HEAD_DIM, 1024, self.theta, device="cuda")
+
+    def params(self):
+        return [self.w_qkv, self.w_o, self.w_gate, self.qn, self.kn]
 
     def qkv(self, x, pos):
         b, s, _ = x.shape
+        if self.fused:
+            return qkv_norm_rope(_linear(x, self.w_qkv), HEADS, KV_HEADS, HEAD_DIM, pos, self.cos, self.sin,
+                                 self.qn, self.kn)
         q, k, v = _linear(x, self.w_qkv).split((HEADS * HEAD_DIM, KV_HEADS * HEAD_DIM, KV_HEADS * HEAD_DIM), -1)
         q, k, v = (t.view(b, s, -1, HEAD_DIM) for t in (q, k, v))  # strided views of the fused output
         q, k = _rms(q, self.qn).to(v.dtype), _rms(k, self.kn).to(v.dtype)
@@ -83,14 +93,17 @@ class Block:
 
     def out(self, x, o):
         b, s, _ = x.shape
-        o = o.reshape(b, s, -1) * torch.sigmoid(_linear(x, self.w_gate))
+        if self.fused:
+            o = output_gate(o.reshape(b, s, -1), _linear(x, self.w_gate))
+        else:
+            o = o.reshape(b, s, -1) * torch.sigmoid(_linear(x, self.w_gate))
         return _linear(o, self.w_o)
 
 
-def _model(seed=0):
+def _model(seed=0, fused=False):
     g = torch.Generator().manual_seed(seed)
     emb = (torch.randn(500, HIDDEN, generator=g) * 0.5).to(torch.bfloat16).cuda()
-    return emb, [Block(g, local=True), Block(g, local=False)]
+    return emb, [Block(g, local=True, fused=fused), Block(g, local=False, fused=fused)]
 
 
 def _full(emb, blocks, ids, attn="kernel"):
@@ -204,13 +217,15 @@ def test_stack_matches_the_fp32_oracle_attention():
     assert_close(o, ref)
 
 
+@pytest.mark.parametrize("fused", [False, True])
 @torch.no_grad()
-def test_decode_step_replays_from_a_graph():
+def test_decode_step_replays_from_a_graph(fused):
     """A decode step (both blocks, static caches written by the kernel) captured in a HIP
     graph: every replay equals the eager step on the same state, bit for bit
-    (tests/test_model.py:121-141), with eager work and synchronizations between replays."""
-    _say("harness: graph replay")
-    emb, blocks = _model()
+    (tests/test_model.py:121-141), with eager work and synchronizations between replays;
+    also with the fused prologue / epilogue kernels in the captured step."""
+    _say(f"harness: graph replay (fused={fused})")
+    emb, blocks = _model(fused=fused)
     b, prompt, steps = 2, 64, 6
     ids = torch.randint(0, 500, (b, prompt + steps), generator=torch.Generator().manual_seed(4)).cuda()
     eager, graphed = StaticDecoder(emb, blocks, b, 128), StaticDecoder(emb, blocks, b, 128)
@@ -241,3 +256,32 @@ def test_decode_step_replays_from_a_graph():
         assert torch.equal(y_graph, y_eager), f"replay at position {t} differs from the eager step"
         eager.seqlens += 1
         graphed.seqlens += 1
+
+
+def test_fused_prologue_epilogue_training_step():
+    """The stack with the fused prologue / epilogue kernels == the stack with the reference's
+    torch ops (mixers.py:85-89, :116-117): outputs, and the gradients of every block parameter
+    and of the input through a fwd+bwd step (the reference's tolerance)."""
+    _say("harness: fused vs composed training step")
+    ids = torch.randint(0, 500, (2, 192), generator=torch.Generator().manual_seed(5)).cuda()
+    results = []
+    for fused in (False, True):
+        emb, blocks = _model(seed=6, fused=fused)
+        leaves = [t.requires_grad_(True) for blk in blocks for t in blk.params()]
+        x0 = emb[ids].detach().requires_grad_(True)
+        b, s = ids.shape
+        pos = torch.arange(s, device="cuda").expand(b, -1)
+        x = x0
+        for blk in blocks:
+            q, k, v = blk.qkv(x, pos)
+            o = flash_attn_func(q, k, v, causal=True, window_size=blk.window)
+            x = x + blk.out(x, o)
+        dy = torch.randn(x.shape, generator=torch.Generator().manual_seed(7)).to(x.dtype).cuda()
+        grads = torch.autograd.grad(x, [x0, *leaves], dy)
+        results.append((x.detach(), grads))
+    (y0, g0), (y1, g1) = results
+    assert_close(y1, y0)
+    names = ["x"] + [f"{n}[{i}]" for i in range(2) for n in ("w_qkv", "w_o", "w_gate", "q_norm", "k_norm")]
+    for name, a, e in zip(names, g1, g0):
+        _say(f"  d{name}: max-abs {(a.float() - e.float()).abs().max().item():.3e} of {e.float().abs().max().item():.3e}")
+        assert_close(a, e)
