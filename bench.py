@@ -405,6 +405,70 @@ def measure_block_io(w, steps: int):
     return out
 
 
+def measure_fused_ce(steps: int, tokens: int = 16384, hidden: int = 1024, vocab: int = 65536, chunk: int = 2048):
+    """fused_linear_cross_entropy at the reference model's head (hidden 1024, tied 64K
+    vocabulary: configs/model/200m.yaml; 2048-token chunks: train/config.py:79) over 16384
+    tokens, bf16 hidden and fp32 weight as under autocast with fp32 master weights. The whole
+    op (3 GEMMs per chunk + the CE row kernel; its backward only scales) and the CE row kernel
+    alone on one chunk (algorithmic bytes: the logits read once and written once). Beside
+    them, the same chunk loop with the CE rows as torch ops (no row kernel)."""
+    from myk_llm_amd.fused_ce import _ce_rows, fused_linear_cross_entropy
+
+    g = torch.Generator(device="cuda").manual_seed(2)
+    h = torch.randn(tokens, hidden, device="cuda", generator=g).to(torch.bfloat16)
+    w = 0.05 * torch.randn(vocab, hidden, device="cuda", generator=g)
+    t = torch.randint(0, vocab, (tokens,), device="cuda", generator=g)
+    t[::9] = -100
+    norm = float((t != -100).sum().item())
+
+    def op():
+        loss, _, _ = fused_linear_cross_entropy(h, w, t, norm, 1e-4, chunk_size=chunk)
+        return loss
+
+    ms = time_events(op, max(5, steps // 5))
+    flops = 6.0 * tokens * hidden * vocab
+
+    logits = (h[:chunk] @ w.to(torch.bfloat16).t()).contiguous()
+    work = logits.clone()
+    ce, lse = torch.empty(chunk, device="cuda"), torch.empty(chunk, device="cuda")
+    tc = t[:chunk]
+
+    def rows():  # rewrites `work` in place each call: same bytes, same work per call
+        _ce_rows(work, tc, ce, lse, 1.0 / norm, 1e-4, -100)
+
+    ms_rows = time_events(rows, max(20, steps))
+    row_bytes = 2 * chunk * vocab * 2
+
+    wb = w.to(torch.bfloat16)
+
+    def torch_chain():
+        gh = torch.empty(tokens, hidden, device="cuda", dtype=torch.bfloat16)
+        gw = torch.zeros(vocab, hidden, device="cuda")
+        total = torch.zeros((), device="cuda")
+        for s0 in range(0, tokens, chunk):
+            hc = h[s0:s0 + chunk]
+            lg = (hc @ wb.t()).float()
+            tt = t[s0:s0 + chunk]
+            valid = tt != -100
+            ls = torch.logsumexp(lg, -1)
+            total += torch.where(valid, ls - lg.gather(1, tt.clamp_min(0)[:, None])[:, 0], 0.0).sum()
+            p = torch.softmax(lg, -1) * ((1 + 2e-4 * ls) / norm)[:, None]
+            p.scatter_add_(1, tt.clamp_min(0)[:, None], torch.where(valid, -1.0 / norm, 0.0)[:, None])
+            p = (p * valid[:, None]).to(torch.bfloat16)
+            torch.mm(p, wb, out=gh[s0:s0 + chunk])
+            gw.add_(p.t() @ hc)
+        return total
+
+    ms_torch = time_events(torch_chain, max(3, steps // 10))
+    return {"shape": {"tokens": tokens, "hidden": hidden, "vocab": vocab, "chunk": chunk},
+            "ms": round(ms, 4), "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1),
+            "frac_of_bf16_peak": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+            "ce_rows_us": round(ms_rows * 1e3, 2), "ce_rows_bytes": row_bytes,
+            "ce_rows_GB/s": round(row_bytes / (ms_rows * 1e-3) / 1e9, 1),
+            "ce_rows_frac_of_hbm_peak": round(row_bytes / (ms_rows * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "torch_ce_rows_chain_ms": round(ms_torch, 4)}
+
+
 # --- CPU baseline ---------------------------------------------------------------------------------
 
 
@@ -474,6 +538,8 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only: no other configs, no CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-only", action="store_true", help="only the decode configs (for profiling)")
+    ap.add_argument("--fused-ce-only", action="store_true",
+                    help="only the fused linear + cross-entropy at the reference model's head (for profiling)")
     ap.add_argument("--block-io-only", action="store_true",
                     help="only the attention-block prologue / epilogue kernels at the cfg3 shape (for profiling)")
     ap.add_argument("--graph", action="store_true", help="time prefill steps as HIP graph replays instead of eager calls")
@@ -507,6 +573,9 @@ def main():
                          "ms_single_call_graph": round(m1, 5), "splits": splits,
                          "kernel_ms": {k: round(v, 5) for k, v in kk.items()}}
         print(json.dumps({"decode_only": out}), flush=True)
+        return
+    if args.fused_ce_only:
+        print(json.dumps({"fused_ce_200m_head": measure_fused_ce(args.steps)}), flush=True)
         return
     if args.block_io_only:
         print(json.dumps({"block_io_cfg3": measure_block_io(W["cfg3"], args.steps)}), flush=True)
@@ -550,6 +619,9 @@ def main():
                                           "traffic": profiled_traffic("decode_splitk", "cfg5_decode")
                                           if name == "cfg5" else None}}
             log(f"  {m * 1e3:.1f} us per layer ({m1 * 1e3:.1f} us as a one-call graph), {gbs:.0f} GB/s; kernels (ms): " + ", ".join(f"{k}={v:.4f}" for k, v in kk.items()))
+        log("fused linear + cross-entropy at the reference model's head")
+        configs["fused_ce_200m_head"] = measure_fused_ce(args.steps)
+        log("  " + json.dumps(configs["fused_ce_200m_head"]))
         log("attention-block prologue / epilogue at the cfg3 shape")
         configs["block_io_cfg3"] = measure_block_io(W["cfg3"], args.steps)
         log("  " + json.dumps(configs["block_io_cfg3"]))

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define MYKFA_ABI_VERSION 4
+#define MYKFA_ABI_VERSION 5
 #define MYKFA_UNBOUNDED (1 << 30) /* flash_attn.py:32 (_UNBOUNDED) */
 
 /* Status codes. */
@@ -238,6 +238,31 @@ typedef struct mykfa_gate_params {
     int32_t dtype;
 } mykfa_gate_params;
 
+/*
+ * Cross-entropy rows of the fused linear + cross-entropy (replaces _ce_kernel,
+ * ops/fused_ce.py:20-67). For each row r of `logits` (a chunk of hidden @ weight^T):
+ *   lse[r] = logsumexp(logits[r]),  ce[r] = lse[r] - logits[r, targets[r]]   (fp32), and
+ *   logits[r] overwritten with softmax(logits[r]) * scale * (1 + 2 z_coef lse[r])
+ *                                 - scale * onehot(targets[r])   (the gradient of
+ *   scale * (ce + z_coef * lse^2) with respect to the logits);
+ * rows whose target equals ignore_index get zeros and ce = lse = 0. A target outside
+ * [0, vocab) other than ignore_index gives ce = NaN (no class to subtract).
+ * targets are int64; the row stride is in elements.
+ */
+typedef struct mykfa_ce_params {
+    void* logits;
+    const int64_t* targets;
+    float* ce;
+    float* lse;
+    int64_t row_stride;
+    int64_t rows;
+    int32_t vocab;
+    int32_t ignore_index;
+    float scale;
+    float z_coef;
+    int32_t dtype;
+} mykfa_ce_params;
+
 /* ---- version / errors ------------------------------------------------------------- */
 int mykfa_abi_version(void);
 const char* mykfa_version(void);
@@ -317,6 +342,13 @@ int mykfa_qk_prologue_bwd(const mykfa_qk_prologue_bwd_params* p, void* workspace
 int mykfa_gate_fwd(const mykfa_gate_params* p, mykfa_stream_t stream);
 /* dx, dgate from dy (autograd of mixers.py:116-117). */
 int mykfa_gate_bwd(const mykfa_gate_params* p, mykfa_stream_t stream);
+
+/* ---- fused linear + cross-entropy: the row kernel ----------------------------------- */
+size_t mykfa_sizeof_ce_params(void);
+int mykfa_validate_ce(const mykfa_ce_params* p);
+/* lse, ce and the in-place logits gradient of each row (replaces _ce_kernel,
+ * ops/fused_ce.py:20-67; launched per token chunk by _FusedLinearCE.forward, :78-89). */
+int mykfa_ce_rows(const mykfa_ce_params* p, mykfa_stream_t stream);
 
 #ifdef __cplusplus
 }

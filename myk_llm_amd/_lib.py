@@ -12,7 +12,7 @@ import os
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmykfa.so"
-ABI_VERSION = 4  # MYKFA_ABI_VERSION
+ABI_VERSION = 5  # MYKFA_ABI_VERSION
 
 OK = 0
 ERR_INVALID = 1
@@ -113,6 +113,14 @@ class GateParams(ctypes.Structure):
     ]
 
 
+class CeParams(ctypes.Structure):
+    _fields_ = [
+        ("logits", _ptr), ("targets", _ptr), ("ce", _ptr), ("lse", _ptr),
+        ("row_stride", _i64), ("rows", _i64), ("vocab", _i32), ("ignore_index", _i32),
+        ("scale", _f32), ("z_coef", _f32), ("dtype", _i32),
+    ]
+
+
 # Every symbol include/mykfa.h declares, with (restype, argtypes).
 SIGNATURES = {
     "mykfa_abi_version": (ctypes.c_int, []),
@@ -148,6 +156,9 @@ SIGNATURES = {
     "mykfa_qk_prologue_bwd": (ctypes.c_int, [ctypes.POINTER(QkPrologueBwdParams), _ptr, ctypes.c_size_t, _ptr]),
     "mykfa_gate_fwd": (ctypes.c_int, [ctypes.POINTER(GateParams), _ptr]),
     "mykfa_gate_bwd": (ctypes.c_int, [ctypes.POINTER(GateParams), _ptr]),
+    "mykfa_sizeof_ce_params": (ctypes.c_size_t, []),
+    "mykfa_validate_ce": (ctypes.c_int, [ctypes.POINTER(CeParams)]),
+    "mykfa_ce_rows": (ctypes.c_int, [ctypes.POINTER(CeParams), _ptr]),
 }
 
 _STRUCT_SIZES = {
@@ -158,6 +169,7 @@ _STRUCT_SIZES = {
     "mykfa_sizeof_qk_prologue_params": QkPrologueParams,
     "mykfa_sizeof_qk_prologue_bwd_params": QkPrologueBwdParams,
     "mykfa_sizeof_gate_params": GateParams,
+    "mykfa_sizeof_ce_params": CeParams,
 }
 
 _lib: ctypes.CDLL | None = None

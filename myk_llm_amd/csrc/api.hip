@@ -263,6 +263,26 @@ int check_gate(const mykfa_gate_params* p, bool backward) {
     return check_view(p->dgate, 0, p->dgate_row_stride, 0, "dgate");
 }
 
+// ops/fused_ce.py:20-33 (the row kernel's arguments).
+int check_ce(const mykfa_ce_params* p) {
+    if (p == nullptr) return fail(MYKFA_ERR_INVALID, "params is NULL");
+    if (p->dtype != MYKFA_BF16 && p->dtype != MYKFA_FP16)
+        return fail(MYKFA_ERR_UNSUPPORTED, "cross entropy needs bf16/fp16 logits; got dtype code %d", p->dtype);
+    if (p->rows < 0 || p->rows > 0x7fffffffLL)
+        return fail(MYKFA_ERR_INVALID, "rows must lie in [0, 2^31); got %lld", (long long)p->rows);
+    if (p->vocab <= 0) return fail(MYKFA_ERR_INVALID, "vocab must be positive; got %d", p->vocab);
+    if (p->rows == 0) return MYKFA_OK;
+    if (p->row_stride < p->vocab)
+        return fail(MYKFA_ERR_INVALID, "row_stride %lld is smaller than vocab %d", (long long)p->row_stride, p->vocab);
+    if (p->logits == nullptr || p->targets == nullptr || p->ce == nullptr || p->lse == nullptr)
+        return fail(MYKFA_ERR_INVALID, "logits, targets, ce and lse must be non-NULL");
+    if ((reinterpret_cast<uintptr_t>(p->logits) & 1) != 0 || (reinterpret_cast<uintptr_t>(p->targets) & 7) != 0 ||
+        (reinterpret_cast<uintptr_t>(p->ce) & 3) != 0 || (reinterpret_cast<uintptr_t>(p->lse) & 3) != 0)
+        return fail(MYKFA_ERR_INVALID, "misaligned logits / targets / ce / lse");
+    if (!(p->scale == p->scale) || !(p->z_coef == p->z_coef)) return fail(MYKFA_ERR_INVALID, "scale or z_coef is NaN");
+    return MYKFA_OK;
+}
+
 hipStream_t as_stream(mykfa_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
 int choose_splits(const mykfa_decode_params* p) {
@@ -437,6 +457,20 @@ int mykfa_gate_bwd(const mykfa_gate_params* p, mykfa_stream_t stream) {
     if (rc) return rc;
     if (p->rows == 0) return ok();
     return launched(mykfa::launch_gate(*p, true, as_stream(stream)), "mykfa_gate_bwd");
+}
+
+size_t mykfa_sizeof_ce_params(void) { return sizeof(mykfa_ce_params); }
+
+int mykfa_validate_ce(const mykfa_ce_params* p) {
+    int rc = check_ce(p);
+    return rc ? rc : ok();
+}
+
+int mykfa_ce_rows(const mykfa_ce_params* p, mykfa_stream_t stream) {
+    int rc = check_ce(p);
+    if (rc) return rc;
+    if (p->rows == 0) return ok();
+    return launched(mykfa::launch_ce_rows(*p, as_stream(stream)), "mykfa_ce_rows");
 }
 
 }  // extern "C"

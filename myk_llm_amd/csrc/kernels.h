@@ -33,4 +33,7 @@ hipError_t launch_qk_prologue_fwd(const mykfa_qk_prologue_params& p, hipStream_t
 hipError_t launch_qk_prologue_bwd(const mykfa_qk_prologue_bwd_params& p, void* ws, hipStream_t stream);
 hipError_t launch_gate(const mykfa_gate_params& p, bool backward, hipStream_t stream);
 
+// Cross-entropy rows of the fused linear + cross-entropy (fused_ce.hip).
+hipError_t launch_ce_rows(const mykfa_ce_params& p, hipStream_t stream);
+
 }  // namespace mykfa

@@ -1,0 +1,165 @@
+"""Parity of the fused linear + cross-entropy (myk_llm_amd.fused_ce, csrc/fused_ce.hip) with
+the CPU oracle (oracle/fused_ce.py) on identical seeded inputs.
+
+- The CE row kernel against the float64 row oracle on the same logits: lse and ce within
+  2e-5 relative (fp32 sums of fp32 exponentials), the in-place gradient within one storage
+  ulp plus 1e-6 * scale (the 16-bit rounding of an fp32 value); both the register-resident
+  path (vocab <= 65536, multiple of 8) and the two-pass path (larger or unaligned rows).
+- The whole op against the reference's own test (tests/test_fused_ce.py:10-38), with its
+  tolerances, and at the reference model's head shape (H = 1024, V = 65536).
+"""
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from _util import storage_ulp
+from myk_llm_amd import _lib
+from myk_llm_amd.fused_ce import _ce_rows, fused_linear_cross_entropy
+from oracle import fused_ce as oc
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.mark.parametrize("rows,vocab,dtype,z", [
+    (64, 1000, torch.bfloat16, 0.0),
+    (37, 4096, torch.bfloat16, 1e-3),
+    (16, 65536, torch.bfloat16, 1e-3),
+    (8, 65536, torch.float16, 0.0),
+    (9, 100000, torch.bfloat16, 1e-4),   # two-pass, 16-byte accesses
+    (11, 1003, torch.bfloat16, 1e-3),    # two-pass, element accesses
+    (5, 8, torch.bfloat16, 0.0),
+])
+def test_ce_rows_match_oracle(rows, vocab, dtype, z):
+    _say(f"ce rows {rows}x{vocab} {dtype} z={z}")
+    g = torch.Generator().manual_seed(rows * 7 + vocab)
+    x = (torch.randn(rows, vocab, generator=g) * 4).to(dtype)
+    t = torch.randint(0, vocab, (rows,), generator=g)
+    t[1::4] = -100
+    scale = 1.0 / 123.0
+    logits = x.cuda()
+    ce = torch.empty(rows, device="cuda")
+    lse = torch.empty(rows, device="cuda")
+    _ce_rows(logits, t.cuda(), ce, lse, scale, z, -100)
+    torch.cuda.synchronize()
+    grad_ref, ce_ref, lse_ref = oc.ce_rows(x.double().numpy(), t.numpy(), scale, z)
+    np.testing.assert_allclose(lse.cpu().double().numpy(), lse_ref, rtol=2e-5, atol=1e-6)
+    np.testing.assert_allclose(ce.cpu().double().numpy(), ce_ref, rtol=2e-5, atol=2e-5)
+    got = logits.float().cpu()
+    ref = torch.tensor(grad_ref)
+    # one storage ulp, floored at the spacing of the type's subnormals (fp16: 2^-24; tiny
+    # probabilities round to those), plus 1e-6 * scale for the fp32 arithmetic
+    sub = 2.0 ** -24 if dtype == torch.float16 else 2.0 ** -133
+    bound = storage_ulp(ref, dtype).double().clamp_min(sub) + 1e-6 * scale
+    err = (got.double() - ref).abs()
+    _say(f"  grad max-abs {err.max().item():.3e}, exact {(err == 0).double().mean().item() * 100:.2f}%")
+    assert (err <= bound).all(), f"{(err > bound).sum().item()} gradient elements beyond one ulp"
+    assert torch.equal(got[1::4], torch.zeros_like(got[1::4]))
+
+
+def test_out_of_range_target_gives_nan_and_stays_in_bounds():
+    x = torch.randn(3, 512).to(torch.bfloat16).cuda()
+    guard = torch.full((2, 512), 7.0, dtype=torch.bfloat16, device="cuda")
+    buf = torch.cat([x, guard])  # rows after the chunk must stay untouched
+    t = torch.tensor([5, 512, -1], device="cuda")
+    ce, lse = torch.empty(3, device="cuda"), torch.empty(3, device="cuda")
+    _ce_rows(buf[:3], t, ce, lse, 1.0, 0.0, -100)
+    torch.cuda.synchronize()
+    assert torch.isfinite(ce[0]) and torch.isnan(ce[1]) and torch.isnan(ce[2])
+    assert torch.equal(buf[3:], guard)
+
+
+def test_deterministic():
+    x = (torch.randn(32, 65536) * 3).to(torch.bfloat16).cuda()
+    t = torch.randint(0, 65536, (32,)).cuda()
+    outs = []
+    for _ in range(3):
+        lg = x.clone()
+        ce, lse = torch.empty(32, device="cuda"), torch.empty(32, device="cuda")
+        _ce_rows(lg, t, ce, lse, 0.01, 1e-3, -100)
+        outs.append((lg, ce, lse))
+    for o in outs[1:]:
+        assert all(torch.equal(a, b) for a, b in zip(o, outs[0]))
+
+
+@pytest.mark.parametrize("z_loss", [0.0, 1e-3])
+def test_matches_reference_loss_and_gradients(z_loss):
+    """tests/test_fused_ce.py:10-38, its shapes, seeds and tolerances."""
+    torch.manual_seed(0)
+    n, h, v = 300, 64, 1000
+    hidden = torch.randn(n, h).cuda().requires_grad_(True)
+    weight = (0.1 * torch.randn(v, h)).cuda().requires_grad_(True)
+    targets = torch.randint(0, v, (n,)).cuda()
+    targets[::7] = -100
+    normalizer = 123.0
+    loss, ce_sum, z_sum = fused_linear_cross_entropy(hidden, weight, targets, normalizer, z_loss, chunk_size=128)
+    loss.backward()
+    grads = hidden.grad.clone(), weight.grad.clone()
+
+    hc = hidden.detach().cpu().requires_grad_(True)
+    wc = weight.detach().cpu().requires_grad_(True)
+    ref, ce_ref = oc.loss_reference(hc, wc, targets.cpu(), normalizer, z_loss)
+    ref.backward()
+    torch.testing.assert_close(loss.cpu(), ref, rtol=1e-3, atol=1e-3)
+    torch.testing.assert_close(ce_sum.cpu(), ce_ref.detach(), rtol=1e-3, atol=1e-2)
+    torch.testing.assert_close(grads[0].cpu(), hc.grad, rtol=2e-2, atol=2e-4)
+    torch.testing.assert_close(grads[1].cpu(), wc.grad, rtol=2e-2, atol=2e-4)
+    valid = targets.cpu() != -100
+    logits = hc.detach().bfloat16().float() @ wc.detach().bfloat16().float().t()
+    z_ref = torch.logsumexp(logits, -1)[valid].square().sum()
+    torch.testing.assert_close(z_sum.cpu(), z_ref, rtol=1e-3, atol=1e-2)
+
+
+def test_model_head_shape():
+    """The reference model's head (hidden 1024, tied 64K vocabulary, configs/model/200m.yaml)
+    on 4096 tokens in 2048-token chunks (train/config.py:79), bf16 hidden as under autocast:
+    loss and gradients against the fp32 reference of tests/test_fused_ce.py:27-33."""
+    _say("fused CE at H=1024, V=65536, 4096 tokens")
+    g = torch.Generator().manual_seed(11)
+    n, h, v = 4096, 1024, 65536
+    hidden = torch.randn(n, h, generator=g).to(torch.bfloat16)
+    weight = (0.05 * torch.randn(v, h, generator=g))
+    targets = torch.randint(0, v, (n,), generator=g)
+    targets[::9] = -100
+    normalizer = float((targets != -100).sum())
+    hd, wd = hidden.cuda().requires_grad_(True), weight.cuda().requires_grad_(True)
+    loss, ce_sum, _ = fused_linear_cross_entropy(hd, wd, targets.cuda(), normalizer, 1e-4)
+    loss.backward()
+    torch.cuda.synchronize()
+    # reference on the GPU in fp32 (bf16-rounded operands, exact in fp32), chunked by rows
+    wb = wd.detach().bfloat16().float()
+    hb = hd.detach().float()
+    ce_tot, z_tot = 0.0, 0.0
+    gh = torch.empty(n, h, device="cuda")
+    gw = torch.zeros(v, h, device="cuda")
+    for s0 in range(0, n, 1024):
+        lg = (hb[s0:s0 + 1024] @ wb.t()).double()
+        tt = targets[s0:s0 + 1024].cuda()
+        valid = tt != -100
+        lse = torch.logsumexp(lg, -1)
+        ce = torch.where(valid, lse - lg.gather(1, tt.clamp_min(0)[:, None])[:, 0], 0.0)
+        ce_tot += ce.sum().item()
+        z_tot += (lse[valid] ** 2).sum().item()
+        p = torch.softmax(lg, -1) * (1 + 2e-4 * lse)[:, None]
+        p[valid.nonzero()[:, 0], tt[valid]] -= 1.0
+        p[~valid] = 0
+        p = (p / normalizer).float()
+        gh[s0:s0 + 1024] = p @ wb
+        gw += p.t() @ hb[s0:s0 + 1024]
+    ref_loss = (ce_tot + 1e-4 * z_tot) / normalizer
+    _say(f"  loss {loss.item():.6f} vs {ref_loss:.6f}; ce_sum {ce_sum.item():.3f} vs {ce_tot:.3f}")
+    assert abs(loss.item() - ref_loss) <= 1e-3 * abs(ref_loss)
+    assert abs(ce_sum.item() - ce_tot) <= 1e-3 * abs(ce_tot)
+    for got, ref, name in ((hd.grad, gh, "d hidden"), (wd.grad, gw, "d weight")):
+        err = (got.float() - ref).abs().max().item()
+        _say(f"  {name}: max-abs {err:.3e} (max |ref| {ref.abs().max().item():.3e})")
+        # the reference's gradient tolerance (tests/test_fused_ce.py:37-38) scaled to the
+        # gradient's magnitude (1 / normalizer here, vs 1 / 123 there)
+        torch.testing.assert_close(got.float(), ref, rtol=2e-2, atol=2e-2 * ref.abs().max().item())
