@@ -334,14 +334,9 @@ __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) pv[r] = fast_exp2(fmaf(s[r], qk_scale, -lsev[r]));
         // Band mask, only on tiles that cross the band edge (flash_attn.py:294-296).
-        if (masked) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int qi = m0 + 16 * (r >> 3) + 8 * g + (r & 7);
-                const int rel = key - qi;
-                pv[r] = (rel >= lo_f && rel <= hi_f && qi < q_len && key < k_len) ? pv[r] : 0.f;
-            }
-        }
+        // Query i is visible from this lane's key iff lo_f <= key - i <= hi_f, i < q_len and
+        // key < k_len: one range of query rows (register r = 8 kb + i is row m0 + 16 kb + 8 g + i).
+        if (masked) mask_runs16(pv, m0 + 8 * g, key - hi_f, key < k_len ? min(key - lo_f, q_len - 1) : key - hi_f - 1);
         s16x8 pb[2], dsb[2];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
@@ -570,14 +565,9 @@ __global__ __launch_bounds__(NW * 64) void bwd_dq_kernel(BwdArgs a) {
                 float pv[16];
 #pragma unroll
                 for (int r = 0; r < 16; ++r) pv[r] = fast_exp2(fmaf(st[r], a.qk_scale, -lse_q));
-                if (masked) {
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int key = n0 + nb * 32 + out_row32(r, g);
-                        const int rel = key - qi;
-                        pv[r] = (rel >= lo_off && rel <= hi_off && key < k_len) ? pv[r] : 0.f;
-                    }
-                }
+                // Key j is visible from this lane's query iff lo_off <= j - qi <= hi_off and
+                // j < k_len: one range (register r holds key n0 + 32 nb + out_row32(r, g)).
+                if (masked) mask_runs16(pv, n0 + nb * 32 + 8 * g, qi + lo_off, min(qi + hi_off, k_len - 1));
 #pragma unroll
                 for (int r = 0; r < 16; ++r) dsv[r] = pv[r] * (dpt[r] - del_q);
             } else {

@@ -404,4 +404,26 @@ __device__ inline int band_hi(int k_len, int q_len, int wr) {
     return v > (1 << 30) ? (1 << 30) : (int)v;
 }
 
+// Band mask of the 16 output registers of a 32x32 MFMA tile, without per-element compares.
+// Register r = 8 h + i (h = 0, 1; i = 0..7) holds index base + 16 h + i of the masked
+// dimension, and the lane's visible indices form one inclusive range [lo, hi] (empty when
+// hi < lo). Each run of 8 gets an 8-bit mask from two clamps; an element is kept by ANDing its
+// bits with the sign-extended mask bit (0 or -1), so masked values become +0 whatever they
+// held. Per-element compares would each produce a 64-bit condition mask in scalar registers;
+// unrolled over 16 elements those exhaust the scalar register file and spill.
+__device__ inline void mask_runs16(float* v, int base, int lo, int hi) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int r0 = base + 16 * h;
+        const int a = min(max(lo - r0, 0), 8);
+        const int b = min(max(hi - r0 + 1, 0), 8);
+        const unsigned bits = ((1u << b) - 1u) & ~((1u << a) - 1u);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int keep = (int)(bits << (31 - i)) >> 31;
+            v[8 * h + i] = __int_as_float(__float_as_int(v[8 * h + i]) & keep);
+        }
+    }
+}
+
 }  // namespace mykfa
