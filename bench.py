@@ -532,7 +532,7 @@ def profiled_traffic(kernel: str, profile: str = "cfg2_fwdbwd"):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="cfg2")
     ap.add_argument("--quick", action="store_true", help="headline only: no other configs, no CPU baseline")

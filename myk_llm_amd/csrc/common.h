@@ -407,11 +407,12 @@ __device__ inline int band_hi(int k_len, int q_len, int wr) {
 // Band mask of the 16 output registers of a 32x32 MFMA tile, without per-element compares.
 // Register r = 8 h + i (h = 0, 1; i = 0..7) holds index base + 16 h + i of the masked
 // dimension, and the lane's visible indices form one inclusive range [lo, hi] (empty when
-// hi < lo). Each run of 8 gets an 8-bit mask from two clamps; an element is kept by ANDing its
-// bits with the sign-extended mask bit (0 or -1), so masked values become +0 whatever they
-// held. Per-element compares would each produce a 64-bit condition mask in scalar registers;
-// unrolled over 16 elements those exhaust the scalar register file and spill.
-__device__ inline void mask_runs16(float* v, int base, int lo, int hi) {
+// hi < lo). Each run of 8 gets an 8-bit mask from two clamps; an element is kept by a bit
+// select with the sign-extended mask bit (0 or -1): masked elements become the float whose
+// bits are `fill` (+0 by default; 0xff800000 is -inf) whatever they held. Per-element compares
+// would each produce a 64-bit condition mask in scalar registers; unrolled over 16 elements
+// those exhaust the scalar register file and spill.
+__device__ inline void mask_runs16(float* v, int base, int lo, int hi, unsigned fill = 0u) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const int r0 = base + 16 * h;
@@ -420,8 +421,8 @@ __device__ inline void mask_runs16(float* v, int base, int lo, int hi) {
         const unsigned bits = ((1u << b) - 1u) & ~((1u << a) - 1u);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const int keep = (int)(bits << (31 - i)) >> 31;
-            v[8 * h + i] = __int_as_float(__float_as_int(v[8 * h + i]) & keep);
+            const unsigned keep = (unsigned)((int)(bits << (31 - i)) >> 31);
+            v[8 * h + i] = __uint_as_float((__float_as_uint(v[8 * h + i]) & keep) | (fill & ~keep));
         }
     }
 }

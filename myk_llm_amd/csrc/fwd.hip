@@ -161,15 +161,20 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdArgs a) {
             }
         }
         // Band mask, only on tiles that cross the band edge (flash_attn.py:140-145).
+        // Key j is visible from this lane's query iff lo_off <= j - qi <= hi_off and j < k_len:
+        // one range (register r of block nb holds key n0 + 32 nb + out_row32(r, g)); masked
+        // scores become -inf.
         if (masked) {
+            const int vis_lo = qi + lo_off, vis_hi = min(qi + hi_off, k_len - 1);
 #pragma unroll
-            for (int nb = 0; nb < NB; ++nb)
+            for (int nb = 0; nb < NB; ++nb) {
+                float sv[16];
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int key = n0 + nb * 32 + out_row32(r, g);
-                    const int rel = key - qi;
-                    if (!(rel >= lo_off && rel <= hi_off && key < k_len)) st[nb][r] = -INFINITY;
-                }
+                for (int r = 0; r < 16; ++r) sv[r] = st[nb][r];
+                mask_runs16(sv, n0 + nb * 32 + 8 * g, vis_lo, vis_hi, 0xff800000u);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) st[nb][r] = sv[r];
+            }
         }
         // Online softmax (flash_attn.py:90-96). The row max is taken on the raw scores (c > 0)
         // and the scale is folded into one FMA per score: p = exp2(s c - m).
