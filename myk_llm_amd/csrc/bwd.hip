@@ -148,9 +148,13 @@ __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
     const int ntiles = (bs > 0 && wr.hi > wr.lo) ? (wr.hi - wr.lo + BMQ - 1) / BMQ : 0;
     const int iters = ntiles * (a.group / hpw);
 
-    // K, V rows of this wave as B operands: lane holds K[nw0 + l32][16 kk + 8 g + i].
+    // K, V rows of this wave as B operands: lane holds K[nw0 + l32][16 kk + 8 g + i]. At
+    // D <= 128 they are loaded after the ring's first tiles are issued, so the two latencies
+    // overlap: the compiler's own waits for these loads count only loads issued after them,
+    // and the older ring loads only lower the counter, so those waits stay exact. (At D = 256
+    // the compiler crashes on that order; there they load first and land before the ring.)
     s16x8 kop[KD], vop[KD];
-    {
+    auto load_kv = [&]() {
         const int key = nw0 + l32;
         const uint16_t* kp = a.k + (int64_t)b * a.kbs + (ks.tok0 + key) * a.kts + (int64_t)kvh * a.khs;
         const uint16_t* vp = a.v + (int64_t)b * a.vbs + (ks.tok0 + key) * a.vts + (int64_t)kvh * a.vhs;
@@ -160,8 +164,11 @@ __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
             kop[kk] = key < k_len ? ld16(kp + 16 * kk + 8 * g) : z;
             vop[kk] = key < k_len ? ld16(vp + 16 * kk + 8 * g) : z;
         }
+    };
+    if constexpr (D > 128) {
+        load_kv();
+        wait_vmcnt<0>();  // K/V landed before the ring's loads share the counter
     }
-    wait_vmcnt<0>();  // K/V landed before the ring's loads share the counter
     // Output rows of this lane's key, formed here so that no kernel argument stays live
     // across the main loop (they would be spilled from scalar registers).
     const int out_key = nw0 + l32;
@@ -277,6 +284,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
 #pragma unroll
     for (int t = 0; t < STAGES; ++t)
         if (t < iters) issue();
+    if constexpr (D <= 128) load_kv();
 
     int cur_tile = 0, cur_stage = 0;
     for (int it = 0; it < iters; ++it) {
