@@ -469,6 +469,38 @@ def measure_fused_ce(steps: int, tokens: int = 16384, hidden: int = 1024, vocab:
             "torch_ce_rows_chain_ms": round(ms_torch, 4)}
 
 
+def measure_syrk(steps: int):
+    """Muon's batched SYRK (x x^T over lower-triangular 128 x 128 tiles) and one 5-step
+    Newton-Schulz orthogonalization at buckets of the reference model (9 matrices of
+    1024 x 4096 and 1024 x 1024; configs/model/200m.yaml), beside torch's full batched product
+    (hipBLASLt bmm of x with a contiguous x^T) on the same GPU. TFLOP/s count the products
+    the kernel executes (2 M'^2 K per lower tile, M' = 128), the MFMA roofline's work; the
+    full-GEMM-equivalent rate (2 M^2 K) is given too."""
+    from myk_llm_amd.muon import batched_newton_schulz_orthogonalize, batched_syrk
+
+    out = {}
+    for b, m, k in ((9, 1024, 4096), (9, 1024, 1024)):
+        g = torch.Generator(device="cuda").manual_seed(3)
+        x = (torch.randn(b, m, k, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+        gram = torch.empty(b, m, m, device="cuda", dtype=torch.bfloat16)
+        ms = time_events(lambda: batched_syrk(x, out=gram), max(20, steps // 4))
+        xt = x.transpose(-2, -1).contiguous()
+        ms_bmm = time_events(lambda: torch.bmm(x, xt), max(20, steps // 4))
+        t = (m + 127) // 128
+        executed = 2.0 * b * (t * (t + 1) // 2) * 128 * 128 * k
+        full = 2.0 * b * m * m * k
+        key = f"b{b}_m{m}_k{k}"
+        out[key] = {"us": round(ms * 1e3, 2), "TFLOP/s_executed": round(executed / (ms * 1e-3) / 1e12, 1),
+                    "frac_of_bf16_peak": round(executed / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                    "TFLOP/s_full_gemm_equivalent": round(full / (ms * 1e-3) / 1e12, 1),
+                    "torch_bmm_full_us": round(ms_bmm * 1e3, 2)}
+        if k == 4096:
+            mats = (torch.randn(b, m, k, device="cuda", generator=g)).to(torch.bfloat16)
+            out[key]["newton_schulz_5_steps_ms"] = round(
+                time_events(lambda: batched_newton_schulz_orthogonalize(mats.clone(), 5), 10), 4)
+    return out
+
+
 # --- CPU baseline ---------------------------------------------------------------------------------
 
 
@@ -538,6 +570,7 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only: no other configs, no CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-only", action="store_true", help="only the decode configs (for profiling)")
+    ap.add_argument("--syrk-only", action="store_true", help="only Muon's batched SYRK (for profiling)")
     ap.add_argument("--fused-ce-only", action="store_true",
                     help="only the fused linear + cross-entropy at the reference model's head (for profiling)")
     ap.add_argument("--block-io-only", action="store_true",
@@ -573,6 +606,9 @@ def main():
                          "ms_single_call_graph": round(m1, 5), "splits": splits,
                          "kernel_ms": {k: round(v, 5) for k, v in kk.items()}}
         print(json.dumps({"decode_only": out}), flush=True)
+        return
+    if args.syrk_only:
+        print(json.dumps({"muon_syrk": measure_syrk(args.steps)}), flush=True)
         return
     if args.fused_ce_only:
         print(json.dumps({"fused_ce_200m_head": measure_fused_ce(args.steps)}), flush=True)
@@ -622,6 +658,9 @@ def main():
         log("fused linear + cross-entropy at the reference model's head")
         configs["fused_ce_200m_head"] = measure_fused_ce(args.steps)
         log("  " + json.dumps(configs["fused_ce_200m_head"]))
+        log("Muon batched SYRK and Newton-Schulz")
+        configs["muon_syrk"] = measure_syrk(args.steps)
+        log("  " + json.dumps(configs["muon_syrk"]))
         log("attention-block prologue / epilogue at the cfg3 shape")
         configs["block_io_cfg3"] = measure_block_io(W["cfg3"], args.steps)
         log("  " + json.dumps(configs["block_io_cfg3"]))

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define MYKFA_ABI_VERSION 5
+#define MYKFA_ABI_VERSION 6
 #define MYKFA_UNBOUNDED (1 << 30) /* flash_attn.py:32 (_UNBOUNDED) */
 
 /* Status codes. */
@@ -263,6 +263,31 @@ typedef struct mykfa_ce_params {
     int32_t dtype;
 } mykfa_ce_params;
 
+/*
+ * Batched symmetric rank-K product of Muon's Newton-Schulz iteration (replaces
+ * _batched_syrk_kernel, ops/muon.py:28-104):
+ *   out[b] = alpha * x[b] x[b]^T + beta * bias[b]     x (batch, m, k), out (batch, m, m), bf16;
+ * the lower-triangular tiles are computed and mirrored into the upper triangle (bias is read
+ * at the computed positions, so it must be symmetric for a symmetric result, as in the
+ * reference). Row strides in elements; k must be a multiple of 32 (callers pad with zero
+ * columns); x 16-byte aligned with a row stride that is a multiple of 8; out 8-byte aligned
+ * with a row stride that is a multiple of 4; bias NULL for none.
+ */
+typedef struct mykfa_syrk_params {
+    const void* x;
+    const void* bias;
+    void* out;
+    int64_t x_batch_stride, x_row_stride;
+    int64_t bias_batch_stride, bias_row_stride;
+    int64_t out_batch_stride, out_row_stride;
+    int32_t batch;
+    int32_t m;
+    int32_t k;
+    float alpha;
+    float beta;
+    int32_t dtype; /* MYKFA_BF16 */
+} mykfa_syrk_params;
+
 /* ---- version / errors ------------------------------------------------------------- */
 int mykfa_abi_version(void);
 const char* mykfa_version(void);
@@ -349,6 +374,13 @@ int mykfa_validate_ce(const mykfa_ce_params* p);
 /* lse, ce and the in-place logits gradient of each row (replaces _ce_kernel,
  * ops/fused_ce.py:20-67; launched per token chunk by _FusedLinearCE.forward, :78-89). */
 int mykfa_ce_rows(const mykfa_ce_params* p, mykfa_stream_t stream);
+
+/* ---- Muon: batched SYRK ------------------------------------------------------------ */
+size_t mykfa_sizeof_syrk_params(void);
+int mykfa_validate_syrk(const mykfa_syrk_params* p);
+/* out = alpha x x^T + beta bias over lower-triangular tiles (replaces _batched_syrk_kernel,
+ * ops/muon.py:28-104, and its launcher batched_syrk, :107-143). */
+int mykfa_syrk(const mykfa_syrk_params* p, mykfa_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -12,7 +12,7 @@ import os
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmykfa.so"
-ABI_VERSION = 5  # MYKFA_ABI_VERSION
+ABI_VERSION = 6  # MYKFA_ABI_VERSION
 
 OK = 0
 ERR_INVALID = 1
@@ -121,6 +121,16 @@ class CeParams(ctypes.Structure):
     ]
 
 
+class SyrkParams(ctypes.Structure):
+    _fields_ = [
+        ("x", _ptr), ("bias", _ptr), ("out", _ptr),
+        ("x_batch_stride", _i64), ("x_row_stride", _i64),
+        ("bias_batch_stride", _i64), ("bias_row_stride", _i64),
+        ("out_batch_stride", _i64), ("out_row_stride", _i64),
+        ("batch", _i32), ("m", _i32), ("k", _i32), ("alpha", _f32), ("beta", _f32), ("dtype", _i32),
+    ]
+
+
 # Every symbol include/mykfa.h declares, with (restype, argtypes).
 SIGNATURES = {
     "mykfa_abi_version": (ctypes.c_int, []),
@@ -159,6 +169,9 @@ SIGNATURES = {
     "mykfa_sizeof_ce_params": (ctypes.c_size_t, []),
     "mykfa_validate_ce": (ctypes.c_int, [ctypes.POINTER(CeParams)]),
     "mykfa_ce_rows": (ctypes.c_int, [ctypes.POINTER(CeParams), _ptr]),
+    "mykfa_sizeof_syrk_params": (ctypes.c_size_t, []),
+    "mykfa_validate_syrk": (ctypes.c_int, [ctypes.POINTER(SyrkParams)]),
+    "mykfa_syrk": (ctypes.c_int, [ctypes.POINTER(SyrkParams), _ptr]),
 }
 
 _STRUCT_SIZES = {
@@ -170,6 +183,7 @@ _STRUCT_SIZES = {
     "mykfa_sizeof_qk_prologue_bwd_params": QkPrologueBwdParams,
     "mykfa_sizeof_gate_params": GateParams,
     "mykfa_sizeof_ce_params": CeParams,
+    "mykfa_sizeof_syrk_params": SyrkParams,
 }
 
 _lib: ctypes.CDLL | None = None

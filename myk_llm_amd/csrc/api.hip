@@ -283,6 +283,32 @@ int check_ce(const mykfa_ce_params* p) {
     return MYKFA_OK;
 }
 
+// ops/muon.py:107-143 (batched_syrk's arguments) with this kernel's layout rules.
+int check_syrk(const mykfa_syrk_params* p) {
+    if (p == nullptr) return fail(MYKFA_ERR_INVALID, "params is NULL");
+    if (p->dtype != MYKFA_BF16) return fail(MYKFA_ERR_UNSUPPORTED, "batched SYRK needs bf16 x; got dtype code %d", p->dtype);
+    if (p->batch < 0 || p->m < 0 || p->k < 0)
+        return fail(MYKFA_ERR_INVALID, "negative shape (batch %d, m %d, k %d)", p->batch, p->m, p->k);
+    if (p->batch > 65535) return fail(MYKFA_ERR_UNSUPPORTED, "batch %d exceeds the grid limit 65535", p->batch);
+    if (p->k % 32 != 0) return fail(MYKFA_ERR_UNSUPPORTED, "k (%d) must be a multiple of 32: pad x with zero columns", p->k);
+    if (!(p->alpha == p->alpha) || !(p->beta == p->beta)) return fail(MYKFA_ERR_INVALID, "alpha or beta is NaN");
+    if (p->batch == 0 || p->m == 0) return MYKFA_OK;
+    if (p->out == nullptr || (reinterpret_cast<uintptr_t>(p->out) & 7) != 0)
+        return fail(MYKFA_ERR_INVALID, "out must be non-NULL and 8-byte aligned");
+    if (p->out_row_stride < p->m || (p->out_row_stride & 3) != 0 || p->out_batch_stride < 0)
+        return fail(MYKFA_ERR_INVALID, "out row stride %lld must be >= m and a multiple of 4", (long long)p->out_row_stride);
+    if (p->bias != nullptr && ((reinterpret_cast<uintptr_t>(p->bias) & 1) != 0 || p->bias_row_stride < 0 ||
+                               p->bias_batch_stride < 0))
+        return fail(MYKFA_ERR_INVALID, "bias must be 2-byte aligned with non-negative strides");
+    if (p->k == 0) return MYKFA_OK;
+    if (p->x == nullptr || !aligned16(p->x)) return fail(MYKFA_ERR_INVALID, "x must be non-NULL and 16-byte aligned");
+    if (p->x_row_stride < p->k || (p->x_row_stride & 7) != 0 || p->x_batch_stride < 0)
+        return fail(MYKFA_ERR_INVALID, "x row stride %lld must be >= k and a multiple of 8", (long long)p->x_row_stride);
+    if ((127 * p->x_row_stride + p->k) * 2 > 0x7fffffffLL)
+        return fail(MYKFA_ERR_UNSUPPORTED, "128 rows of x at row stride %lld span more than 2 GiB", (long long)p->x_row_stride);
+    return MYKFA_OK;
+}
+
 hipStream_t as_stream(mykfa_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
 int choose_splits(const mykfa_decode_params* p) {
@@ -457,6 +483,20 @@ int mykfa_gate_bwd(const mykfa_gate_params* p, mykfa_stream_t stream) {
     if (rc) return rc;
     if (p->rows == 0) return ok();
     return launched(mykfa::launch_gate(*p, true, as_stream(stream)), "mykfa_gate_bwd");
+}
+
+size_t mykfa_sizeof_syrk_params(void) { return sizeof(mykfa_syrk_params); }
+
+int mykfa_validate_syrk(const mykfa_syrk_params* p) {
+    int rc = check_syrk(p);
+    return rc ? rc : ok();
+}
+
+int mykfa_syrk(const mykfa_syrk_params* p, mykfa_stream_t stream) {
+    int rc = check_syrk(p);
+    if (rc) return rc;
+    if (p->batch == 0 || p->m == 0) return ok();
+    return launched(mykfa::launch_syrk(*p, as_stream(stream)), "mykfa_syrk");
 }
 
 size_t mykfa_sizeof_ce_params(void) { return sizeof(mykfa_ce_params); }

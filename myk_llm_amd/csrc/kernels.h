@@ -36,4 +36,7 @@ hipError_t launch_gate(const mykfa_gate_params& p, bool backward, hipStream_t st
 // Cross-entropy rows of the fused linear + cross-entropy (fused_ce.hip).
 hipError_t launch_ce_rows(const mykfa_ce_params& p, hipStream_t stream);
 
+// Batched SYRK of Muon's Newton-Schulz iteration (syrk.hip).
+hipError_t launch_syrk(const mykfa_syrk_params& p, hipStream_t stream);
+
 }  // namespace mykfa

@@ -33,7 +33,7 @@ def test_every_declared_symbol_is_exported_and_bound(L):
 
 
 def test_version_and_struct_sizes(L):
-    assert L.mykfa_abi_version() == _lib.ABI_VERSION == 5
+    assert L.mykfa_abi_version() == _lib.ABI_VERSION == 6
     assert b"gfx950" in L.mykfa_version()
     assert L.mykfa_sizeof_fwd_params() == ctypes.sizeof(_lib.FwdParams)
     assert L.mykfa_sizeof_bwd_params() == ctypes.sizeof(_lib.BwdParams)
@@ -43,6 +43,7 @@ def test_version_and_struct_sizes(L):
     assert L.mykfa_sizeof_qk_prologue_bwd_params() == ctypes.sizeof(_lib.QkPrologueBwdParams)
     assert L.mykfa_sizeof_gate_params() == ctypes.sizeof(_lib.GateParams)
     assert L.mykfa_sizeof_ce_params() == ctypes.sizeof(_lib.CeParams)
+    assert L.mykfa_sizeof_syrk_params() == ctypes.sizeof(_lib.SyrkParams)
 
 
 def good_fwd():
