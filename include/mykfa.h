@@ -269,7 +269,7 @@ typedef struct mykfa_ce_params {
  *   out[b] = alpha * x[b] x[b]^T + beta * bias[b]     x (batch, m, k), out (batch, m, m), bf16;
  * the lower-triangular tiles are computed and mirrored into the upper triangle (bias is read
  * at the computed positions, so it must be symmetric for a symmetric result, as in the
- * reference). Row strides in elements; k must be a multiple of 32 (callers pad with zero
+ * reference). Row strides in elements; k must be a multiple of 64 (callers pad with zero
  * columns); x 16-byte aligned with a row stride that is a multiple of 8; out 8-byte aligned
  * with a row stride that is a multiple of 4; bias NULL for none.
  */

@@ -289,8 +289,12 @@ int check_syrk(const mykfa_syrk_params* p) {
     if (p->dtype != MYKFA_BF16) return fail(MYKFA_ERR_UNSUPPORTED, "batched SYRK needs bf16 x; got dtype code %d", p->dtype);
     if (p->batch < 0 || p->m < 0 || p->k < 0)
         return fail(MYKFA_ERR_INVALID, "negative shape (batch %d, m %d, k %d)", p->batch, p->m, p->k);
-    if (p->batch > 65535) return fail(MYKFA_ERR_UNSUPPORTED, "batch %d exceeds the grid limit 65535", p->batch);
-    if (p->k % 32 != 0) return fail(MYKFA_ERR_UNSUPPORTED, "k (%d) must be a multiple of 32: pad x with zero columns", p->k);
+    {
+        const long long t = ((long long)p->m + 127) / 128;
+        if ((long long)p->batch * (t * (t + 1) / 2) > 0x7ffffff0LL)
+            return fail(MYKFA_ERR_UNSUPPORTED, "batch %d x %lld output tiles exceed the grid limit", p->batch, t * (t + 1) / 2);
+    }
+    if (p->k % 64 != 0) return fail(MYKFA_ERR_UNSUPPORTED, "k (%d) must be a multiple of 64: pad x with zero columns", p->k);
     if (!(p->alpha == p->alpha) || !(p->beta == p->beta)) return fail(MYKFA_ERR_INVALID, "alpha or beta is NaN");
     if (p->batch == 0 || p->m == 0) return MYKFA_OK;
     if (p->out == nullptr || (reinterpret_cast<uintptr_t>(p->out) & 7) != 0)

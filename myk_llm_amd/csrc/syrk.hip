@@ -6,12 +6,14 @@
 // symmetric Bias gives the full symmetric result, as in the reference).
 //
 // One workgroup = one output tile, 4 waves in 2 x 2, each wave a 64 x 64 quarter as 2 x 2
-// blocks of 32x32x16 bf16 MFMA with fp32 accumulation. K advances 32 columns per stage through
-// a 4-stage asynchronous LDS ring (buffer_load ... lds straight into swizzled tiles, 3 stages in
-// flight): stage s holds the 128 x 32 row panels of X at the tile's row block (A) and column
-// block (B). Both MFMA operands are row reads of those panels (X X^T: the B operand of column n
-// is row n of X), taken in the permuted row order under which a 16-byte row read touches every
-// LDS bank once; the permutation is undone when the tile is stored.
+// blocks of 32x32x16 bf16 MFMA with fp32 accumulation. K advances 64 columns per stage through
+// a 2-stage asynchronous LDS ring (buffer_load ... lds straight into swizzled tiles; one stage
+// loads while the other is consumed): a stage holds the 128 x 64 row panels of X at the tile's
+// row block (A) and column block (B). Both MFMA operands are row reads of those panels (X X^T:
+// the B operand of column n is row n of X), taken in the permuted row order under which a
+// 16-byte row read touches every LDS bank once; the permutation is undone when the tile is
+// stored. 64 KB of LDS keeps two workgroups resident per CU (measured: a third 32 KB stage,
+// one workgroup per CU, is 1.8x slower at 9 x 1024 x 4096; 32-column stages 1.2x slower).
 #include "common.h"
 #include "kernels.h"
 
@@ -19,11 +21,11 @@ namespace mykfa {
 namespace {
 
 constexpr int kBM = 128;                             // output tile rows = columns
-constexpr int kBK = 32;                              // K columns per stage
-constexpr int kStages = 4;
+constexpr int kBK = 64;                              // K columns per stage
+constexpr int kStages = 2;
 constexpr int kNW = 4;                               // waves per workgroup (2 x 2)
 constexpr int kCPR = kBK / 8;                        // 16-byte chunks per panel row
-constexpr int kLoadsPerPanel = kBM * kCPR / 64;      // 64-lane loads per 128 x 32 panel
+constexpr int kLoadsPerPanel = kBM * kCPR / 64;      // 64-lane loads per 128 x kBK panel
 constexpr int kLoads = 2 * kLoadsPerPanel / kNW;     // loads per wave per stage (A and B panels)
 static_assert((2 * kLoadsPerPanel) % kNW == 0, "panel loads split evenly over the waves");
 
@@ -47,13 +49,25 @@ __device__ inline float bias_at(const mykfa_syrk_params& p, int bidx, int i, int
     return BF16::to_float(bp[(int64_t)i * p.bias_row_stride + j]);
 }
 
-__global__ __launch_bounds__(kNW * 64) void syrk_kernel(mykfa_syrk_params p) {
+// Workgroup id -> (matrix, tile). The dispatcher deals workgroup i to XCD i % 8; XCD x is
+// given the contiguous run [x * per_xcd, (x + 1) * per_xcd) of the matrix-major unit list, so
+// the tiles of one matrix (8 tiles per row panel of X) share one XCD's L2 instead of each XCD
+// fetching nearly every panel of every matrix. Ids past the last unit do nothing.
+__device__ inline bool syrk_unit(int pid, int per_xcd, int tiles_per_matrix, int units, int& bidx, int& tile) {
+    const int unit = (pid % kXcds) * per_xcd + pid / kXcds;
+    bidx = unit / tiles_per_matrix;
+    tile = unit - bidx * tiles_per_matrix;
+    return unit < units;
+}
+
+__global__ __launch_bounds__(kNW * 64) void syrk_kernel(mykfa_syrk_params p, int per_xcd, int tiles_per_matrix) {
     __shared__ __attribute__((aligned(16))) uint16_t smem[kStages][2][kBM * kBK];
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, l32 = lane & 31, g = lane >> 5;
+    int bidx, tile;
+    if (!syrk_unit(blockIdx.x, per_xcd, tiles_per_matrix, p.batch * tiles_per_matrix, bidx, tile)) return;
     int tm, tn;
-    tile_coord(blockIdx.x, tm, tn);
-    const int bidx = blockIdx.y;
+    tile_coord(tile, tm, tn);
     const int m0 = tm * kBM, n0 = tn * kBM;
 
     // Panel sources: rows [m0, m0 + 128) and [n0, n0 + 128) of X[bidx]; the descriptors cover
@@ -161,8 +175,11 @@ __global__ __launch_bounds__(kNW * 64) void syrk_kernel(mykfa_syrk_params p) {
 
 hipError_t launch_syrk(const mykfa_syrk_params& p, hipStream_t stream) {
     const long long tiles = (long long)(p.m + kBM - 1) / kBM;
-    const dim3 grid((unsigned)(tiles * (tiles + 1) / 2), (unsigned)p.batch);
-    hipLaunchKernelGGL(syrk_kernel, grid, dim3(kNW * 64), 0, stream, p);
+    const long long per_matrix = tiles * (tiles + 1) / 2;
+    const long long per_xcd = (per_matrix * p.batch + kXcds - 1) / kXcds;
+    if (per_xcd * kXcds >= (1ll << 31)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(syrk_kernel, dim3((unsigned)(per_xcd * kXcds)), dim3(kNW * 64), 0, stream, p, (int)per_xcd,
+                       (int)per_matrix);
     return hipGetLastError();
 }
 

@@ -69,14 +69,14 @@ def _good():
 
 @pytest.mark.parametrize("field,value,text", [
     ("dtype", 1, "bf16"),
-    ("k", 4010, "multiple of 32"),
+    ("k", 4000, "multiple of 64"),
     ("m", -1, "negative"),
     ("x", 0x10008, "16-byte aligned"),
     ("x_row_stride", 4100, "multiple of 8"),
     ("out", 0x20004, "8-byte aligned"),
     ("out_row_stride", 1022, "row stride"),
     ("alpha", float("nan"), "NaN"),
-    ("batch", 70000, "grid limit"),
+    ("batch", 1 << 26, "grid limit"),  # 2^26 matrices x 36 tiles > 2^31 workgroups
 ])
 def test_syrk_validation(field, value, text):
     L = _lib.lib()
@@ -96,3 +96,16 @@ def test_cpu_tensors_are_rejected():
 
     with pytest.raises(RuntimeError, match="CUDA-only"):
         batched_syrk(torch.zeros(2, 8, 32, dtype=torch.bfloat16))
+
+
+@pytest.mark.parametrize("shape", [(3, 1024, 512), (2, 100, 52)])
+def test_frobenius_norm_matches_float64(shape):
+    """The driver's two-level fp32 norm (host logic, runs on CPU tensors) against the float64
+    root sum of squares of the same bf16 values."""
+    from myk_llm_amd.muon import _frobenius_norm
+
+    x = torch.randn(*shape, generator=torch.Generator().manual_seed(5)).bfloat16()
+    exact = x.double().square().sum((-2, -1)).sqrt()
+    got = _frobenius_norm(x)
+    assert got.dtype == torch.float32 and got.shape == (shape[0],)
+    assert ((got.double() - exact).abs() <= 1e-6 * exact).all()
