@@ -5,7 +5,7 @@ myk-llm's src/myk_llm/ops/muon.py (exported by ops/__init__.py), same names and 
         out[b] = alpha * x[b] @ x[b]^T + beta * bias[b] in bf16, computing only the
         lower-triangular tiles and mirroring them (ops/muon.py:28-143)
     batched_newton_schulz_orthogonalize(packed, steps, transposed=None, norm_sq=None, eps=1e-7)
-        the quintic Newton-Schulz iteration on a batch of matrices (ops/muon.py:227-268):
+        the quintic Newton-Schulz iteration on a batch of matrices (ops/muon.py:218-268):
         per step G = X X^T and G2 = b G + c G G through batched_syrk, X' = a X + G2 X
 
 The SYRK runs in the hand-written gfx950 kernel of libmykfa.so (csrc/syrk.hip) through its C
@@ -102,7 +102,7 @@ def _frobenius_norm(packed: Tensor) -> Tensor:
 
 def batched_newton_schulz_orthogonalize(packed: Tensor, steps: int, transposed: Optional[bool] = None,
                                         norm_sq: Optional[Tensor] = None, eps: float = 1e-7) -> Tensor:
-    """Batched quintic Newton-Schulz on packed (B, rows, cols) in bf16 (ops/muon.py:227-268).
+    """Batched quintic Newton-Schulz on packed (B, rows, cols) in bf16 (ops/muon.py:218-268).
 
     With norm_sq (per-matrix squared Frobenius norm of packed) the input is scaled by
     1 / max(sqrt(norm_sq), eps) in place, as the reference's _scale_bf16_kernel does;
