@@ -67,7 +67,8 @@ def batched_syrk(x: Tensor, bias: Optional[Tensor] = None, alpha: float = 1.0, b
     xk = _kernel_x(x)
     o = out
     if not (o.stride(2) == 1 and o.stride(1) % 4 == 0 and o.data_ptr() % 8 == 0 and o.stride(1) >= M):
-        o = torch.empty((B, M, M), device=x.device, dtype=torch.bfloat16)
+        # the kernel's mirrored stores are 8 bytes wide: rows padded to a multiple of 4
+        o = torch.empty((B, M, (M + 3) // 4 * 4), device=x.device, dtype=torch.bfloat16)[:, :, :M]
     if bias is not None and (bias.stride(2) != 1 or bias.data_ptr() % 2):
         bias = bias.contiguous()
     p = _lib.SyrkParams()

@@ -38,7 +38,8 @@ def _check_syrk(got, x, bias=None, alpha=1.0, beta=0.0, what=""):
     assert torch.equal(got, got.transpose(-2, -1)), f"{what}: not symmetric"
 
 
-@pytest.mark.parametrize(("m", "k", "transposed"), [(100, 150, False), (256, 512, False), (192, 320, True)])
+@pytest.mark.parametrize(("m", "k", "transposed"), [(100, 150, False), (256, 512, False), (192, 320, True),
+                                                    (130, 192, False)])  # m not a multiple of 4: padded out rows
 def test_batched_syrk_matches_the_product(m, k, transposed):
     _say(f"syrk m={m} k={k} transposed={transposed}")
     g = torch.Generator().manual_seed(0)
