@@ -19,6 +19,10 @@
 namespace mykfa {
 namespace {
 
+// IEEE half bits of x (round to nearest even) and the value of half bits h.
+__device__ inline uint32_t half_bits(float x) { return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x); }
+__device__ inline float half_value(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
+
 constexpr int kCeThreads = 512;
 constexpr int kCeWaves = kCeThreads / 64;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -104,9 +108,15 @@ __device__ inline RowStats finish_stats(const mykfa_ce_params& p, int64_t row, c
     return r;
 }
 
+// bf16 rows keep e^(x - max) as fp16 in the registers that held the logits (values in [0, 1],
+// 2^-11 relative, so the gradient, rounded once more to bf16, stays within 0.75 of its ulp) and
+// form the gradient as p * (scale' / sum): one exponential per logit instead of two, and no
+// per-element target test -- the lane that holds the target column rewrites that one element
+// after its row stores. fp16 rows (whose own ulp is the fp16 one) recompute the exponential.
 template <typename T, int VPT>
 __global__ __launch_bounds__(kCeThreads) void ce_rows_resident_kernel(mykfa_ce_params p) {
     constexpr int NC = VPT / 8;  // 16-byte chunks per lane
+    constexpr bool kKeepP = T::code == MYKFA_BF16;
     __shared__ float red[kCeWaves];
     const int64_t row = blockIdx.x;
     uint16_t* base = static_cast<uint16_t*>(p.logits) + row * p.row_stride;
@@ -117,7 +127,8 @@ __global__ __launch_bounds__(kCeThreads) void ce_rows_resident_kernel(mykfa_ce_p
         return;
     }
     // The target logit is read before the first barrier, so before any lane overwrites the row.
-    const float target_logit = (threadIdx.x == 0 && h.in_range) ? T::to_float(base[h.target]) : 0.f;
+    const bool owner = kKeepP && h.in_range && (int)((h.target / 8) % kCeThreads) == (int)threadIdx.x;
+    const float target_logit = ((threadIdx.x == 0 || owner) && h.in_range) ? T::to_float(base[h.target]) : 0.f;
     s16x8 v[NC];
     float m = -INFINITY;
 #pragma unroll
@@ -136,12 +147,44 @@ __global__ __launch_bounds__(kCeThreads) void ce_rows_resident_kernel(mykfa_ce_p
     for (int j = 0; j < NC; ++j) {
         const int c = (j * kCeThreads + threadIdx.x) * 8;
         if (c < p.vocab) {
+            uint32_t kw[4];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) s += exp_shifted(T::to_float((uint16_t)v[j][i]), m_log2e);
+            for (int i = 0; i < 8; i += 2) {
+                const float e0 = exp_shifted(T::to_float((uint16_t)v[j][i]), m_log2e);
+                const float e1 = exp_shifted(T::to_float((uint16_t)v[j][i + 1]), m_log2e);
+                s += e0;
+                s += e1;
+                kw[i / 2] = half_bits(e0) | (half_bits(e1) << 16);
+            }
+            if constexpr (kKeepP) {
+                const u32x4 keep = {kw[0], kw[1], kw[2], kw[3]};
+                v[j] = __builtin_bit_cast(s16x8, keep);
+            }
         }
     }
     s = block_sum(s, red);
     const RowStats st = finish_stats(p, row, h, m, s, target_logit);
+    if constexpr (kKeepP) {
+        const float ratio = st.softmax_scale / s;  // e^(x - lse) * scale' = e^(x - max) * ratio
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+            const int c = (j * kCeThreads + threadIdx.x) * 8;
+            if (c < p.vocab) {
+                const u32x4 pw = __builtin_bit_cast(u32x4, v[j]);
+                uint32_t ow[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    ow[i] = T::pack2(half_value(pw[i] & 0xffffu) * ratio, half_value(pw[i] >> 16) * ratio);
+                const u32x4 o = {ow[0], ow[1], ow[2], ow[3]};
+                st16(base + c, __builtin_bit_cast(s16x8, o));
+            }
+        }
+        if (owner) {  // after this lane's store of the same 16 bytes
+            const float gt = exp_shifted(target_logit, st.lse_log2e) * st.softmax_scale - p.scale;
+            base[h.target] = (uint16_t)(T::pack2(gt, 0.f) & 0xffffu);
+        }
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < NC; ++j) {
         const int c = (j * kCeThreads + threadIdx.x) * 8;

@@ -32,6 +32,7 @@ def _say(*a):
     (64, 1000, torch.bfloat16, 0.0),
     (37, 4096, torch.bfloat16, 1e-3),
     (16, 65536, torch.bfloat16, 1e-3),
+    (24, 12000, torch.bfloat16, 1e-3),   # 32 columns per lane
     (8, 65536, torch.float16, 0.0),
     (9, 100000, torch.bfloat16, 1e-4),   # two-pass, 16-byte accesses
     (11, 1003, torch.bfloat16, 1e-3),    # two-pass, element accesses
