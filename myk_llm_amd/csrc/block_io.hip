@@ -18,8 +18,8 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kMaxBwdBlocks = 1024;  // weight-gradient partials: one (2, D) fp32 row per workgroup
-constexpr int kHeadsInFlight = 4;     // head rows per lane group whose loads are issued together
-constexpr int kBwdHeadsInFlight = 2;  // (two loads per row in the backward)
+constexpr int kHeadsInFlight = 2;     // head rows per lane group whose loads are issued together (measured: 2 > 4 > 8)
+constexpr int kBwdHeadsInFlight = 2;  // (two loads per row in the backward; 1 and 4 measured slower)
 constexpr int kGateFwdChunks = 1;     // 16-byte chunks per lane per pass (one measured fastest)
 constexpr int kGateBwdChunks = 1;
 
