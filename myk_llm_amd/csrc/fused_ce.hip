@@ -19,10 +19,6 @@
 namespace mykfa {
 namespace {
 
-// IEEE half bits of x (round to nearest even) and the value of half bits h.
-__device__ inline uint32_t half_bits(float x) { return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x); }
-__device__ inline float half_value(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
-
 constexpr int kCeThreads = 512;
 constexpr int kCeWaves = kCeThreads / 64;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -108,11 +104,24 @@ __device__ inline RowStats finish_stats(const mykfa_ce_params& p, int64_t row, c
     return r;
 }
 
-// bf16 rows keep e^(x - max) as fp16 in the registers that held the logits (values in [0, 1],
-// 2^-11 relative, so the gradient, rounded once more to bf16, stays within 0.75 of its ulp) and
-// form the gradient as p * (scale' / sum): one exponential per logit instead of two, and no
-// per-element target test -- the lane that holds the target column rewrites that one element
-// after its row stores. fp16 rows (whose own ulp is the fp16 one) recompute the exponential.
+// bf16 rows keep p = e^(x - max) in the registers that held the logits and form the
+// gradient as p * (scale' / sum): one exponential per logit instead of two, and no per-element
+// target test -- the lane that holds the target column rewrites that one element after its
+// row stores. p lies in [0, 1] and needs no sign, so it is kept in an unsigned 16-bit float
+// of this kernel's own: 6 exponent bits (fp32's biased exponents 64..127, i.e. p in
+// [2^-63, 1]) and fp32's top 10 mantissa bits, rounded: 11 significant bits, 2^-11 relative,
+// over the whole range (fp16 would go subnormal below 2^-14). The gradient, rounded once more
+// to bf16, then stays within 0.625 of its ulp. A 16-byte chunk of 8 logits holding any
+// p < 2^-63 (x more than ~43.7 below the row max) keeps its logits instead (one flag bit per
+// chunk) and recomputes those exponentials from them, as the fp16 rows do for all of theirs.
+constexpr uint32_t kKeepBias = 64u << 23;  // fp32 bits of 2^-63, the code 0
+constexpr float kKeepMin = 0x1p-63f;
+
+__device__ inline uint32_t keep_code(float p) {  // p in [2^-63, 1] -> 16-bit code
+    return (__float_as_uint(p) - kKeepBias + (1u << 12)) >> 13;
+}
+__device__ inline float keep_value(uint32_t code) { return __uint_as_float((code << 13) + kKeepBias); }
+
 template <typename T, int VPT>
 __global__ __launch_bounds__(kCeThreads) void ce_rows_resident_kernel(mykfa_ce_params p) {
     constexpr int NC = VPT / 8;  // 16-byte chunks per lane
@@ -143,22 +152,31 @@ __global__ __launch_bounds__(kCeThreads) void ce_rows_resident_kernel(mykfa_ce_p
     m = block_max(m, red);
     const float m_log2e = m * kLog2e;
     float s = 0.f;
+    uint32_t raw_mask = 0;  // bit j: chunk j still holds its logits (else the codes of p)
+    static_assert(NC <= 32, "one flag bit per chunk");
 #pragma unroll
     for (int j = 0; j < NC; ++j) {
         const int c = (j * kCeThreads + threadIdx.x) * 8;
         if (c < p.vocab) {
-            uint32_t kw[4];
+            float e[8];
 #pragma unroll
-            for (int i = 0; i < 8; i += 2) {
-                const float e0 = exp_shifted(T::to_float((uint16_t)v[j][i]), m_log2e);
-                const float e1 = exp_shifted(T::to_float((uint16_t)v[j][i + 1]), m_log2e);
-                s += e0;
-                s += e1;
-                kw[i / 2] = half_bits(e0) | (half_bits(e1) << 16);
+            for (int i = 0; i < 8; ++i) {
+                e[i] = exp_shifted(T::to_float((uint16_t)v[j][i]), m_log2e);
+                s += e[i];
             }
             if constexpr (kKeepP) {
-                const u32x4 keep = {kw[0], kw[1], kw[2], kw[3]};
-                v[j] = __builtin_bit_cast(s16x8, keep);
+                float lo = e[0];
+#pragma unroll
+                for (int i = 1; i < 8; ++i) lo = fminf(lo, e[i]);
+                if (lo >= kKeepMin) {
+                    uint32_t kw[4];
+#pragma unroll
+                    for (int i = 0; i < 8; i += 2) kw[i / 2] = keep_code(e[i]) | (keep_code(e[i + 1]) << 16);
+                    const u32x4 keep = {kw[0], kw[1], kw[2], kw[3]};
+                    v[j] = __builtin_bit_cast(s16x8, keep);
+                } else {
+                    raw_mask |= 1u << j;  // the chunk keeps its logits
+                }
             }
         }
     }
@@ -172,9 +190,17 @@ __global__ __launch_bounds__(kCeThreads) void ce_rows_resident_kernel(mykfa_ce_p
             if (c < p.vocab) {
                 const u32x4 pw = __builtin_bit_cast(u32x4, v[j]);
                 uint32_t ow[4];
+                if ((raw_mask >> j) & 1u) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    ow[i] = T::pack2(half_value(pw[i] & 0xffffu) * ratio, half_value(pw[i] >> 16) * ratio);
+                    for (int i = 0; i < 4; ++i)
+                        ow[i] = T::pack2(
+                            exp_shifted(T::to_float((uint16_t)(pw[i] & 0xffffu)), st.lse_log2e) * st.softmax_scale,
+                            exp_shifted(T::to_float((uint16_t)(pw[i] >> 16)), st.lse_log2e) * st.softmax_scale);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        ow[i] = T::pack2(keep_value(pw[i] & 0xffffu) * ratio, keep_value(pw[i] >> 16) * ratio);
+                }
                 const u32x4 o = {ow[0], ow[1], ow[2], ow[3]};
                 st16(base + c, __builtin_bit_cast(s16x8, o));
             }

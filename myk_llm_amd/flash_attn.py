@@ -1,28 +1,31 @@
-"""FlashAttention on MI355X (gfx950): the host side of the drop-in for myk-llm's
+"""Host side of the MI355X FlashAttention that stands in for myk-llm's
 src/myk_llm/ops/flash_attn.py.
 
-The three public functions keep the reference's names, signatures, defaults and exception
-types (flash_attn.py:442-490), so model code calls them unchanged:
+Entry points. Their names, positional arguments, defaults and exception types are the
+reference's (flash_attn.py:442-490), so Attention.forward, generate() and the decode
+benchmark call them unchanged:
 
-    flash_attn_func          (batch, seq, heads, head_dim) tensors
-    flash_attn_varlen_func   packed (tokens, heads, head_dim) documents with cu_seqlens
-    flash_attn_with_kvcache  writes new keys/values into a static cache, then attends
-                             (forward only; capturable in a HIP graph)
+    flash_attn_func          dense batches, q (B, Sq, Hq, D) against k / v (B, Sk, Hkv, D)
+    flash_attn_varlen_func   documents packed along the token axis and delimited by int32
+                             cu_seqlens offsets
+    flash_attn_with_kvcache  stores this step's keys / values in a preallocated per-sequence
+                             cache and attends over the grown cache; no gradient, and safe
+                             to capture in a HIP graph
 
-Each also takes a keyword-only ``return_softmax_lse=False``; when True it returns
-``(out, lse)`` where lse is the fp32 base-2 log-sum-exp laid out ``(heads, rows)``, the
-buffer the reference's ``_forward`` produces (flash_attn.py:353-373).
+Keyword-only ``return_softmax_lse=False`` is this build's one addition: with True the call
+also hands back the fp32 log-sum-exp in base 2, one row per query head ``(Hq, rows)``, which is
+what the backward consumes.
 
-Semantics (flash_attn.py:11-18): causal or bidirectional attention, a sliding window, GQA,
-bf16/fp16 inputs, head_dim in {16, 32, 64, 128, 256}; queries are aligned to the END of the
-keys: query i of Lq sits at key position i + Lk - Lq and sees keys j with
-``i + Lk - Lq - window_left <= j <= i + Lk - Lq + window_right``, a side of -1 being
-unbounded and causal forcing window_right = 0.
+Masking. Queries line up with the END of their keys. With Lq queries and Lk keys in a
+sequence, query i may attend to key j exactly when j - i lies in
+[Lk - Lq - left, Lk - Lq + right]; ``window_size = (left, right)`` with -1 meaning no limit on
+that side, and ``causal=True`` pins right to 0. GQA maps query head h to key/value head
+h // (Hq / Hkv). Inputs are bf16 or fp16 with head_dim 16, 32, 64, 128 or 256.
 
-All arithmetic runs in the hand-written gfx950 kernels of libmykfa.so, called through its C
-ABI (include/mykfa.h) on torch's current stream. Python only validates, allocates outputs
-with torch's caching allocator and passes pointers. There is no CPU or PyTorch fallback:
-without the library every call raises.
+Every FLOP runs in libmykfa.so's gfx950 kernels, reached through its C ABI (include/mykfa.h)
+on torch's current stream. This module checks arguments, allocates outputs from torch's
+caching allocator and passes pointers; when the library is missing every call raises, as
+nothing here can compute attention on its own.
 """
 
 from __future__ import annotations
@@ -61,6 +64,17 @@ def _check(q: Tensor, k: Tensor, v: Tensor) -> None:
     if not (q.is_cuda and k.is_cuda and v.is_cuda):
         raise RuntimeError("flash attention is CUDA-only: q, k and v must be GPU (HIP) tensors")
     _check_meta(q, k, v)
+    _same_device(q.device, k=k, v=v)
+
+
+def _same_device(device: torch.device, **tensors: Optional[Tensor]) -> None:
+    """Every tensor the kernels dereference must live on q's GPU. A host tensor (or one on
+    another GPU) would hand the kernel a pointer it cannot read; the reference fails the
+    same calls with a RuntimeError (a device mismatch in torch, or Triton refusing a host
+    pointer), and so does this, before anything is launched."""
+    for name, t in tensors.items():
+        if t is not None and t.device != device:
+            raise RuntimeError(f"every tensor must be on the same GPU: {name} is on {t.device}, expected {device}")
 
 
 def _last_dim_contiguous(x: Tensor) -> Tensor:
@@ -93,7 +107,10 @@ def _dtype_code(dtype: torch.dtype) -> int:
 
 
 def _stream(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """The raw hipStream_t of torch's current stream on device (no Stream object is built:
+    this runs on every launch)."""
+    return torch._C._cuda_getCurrentRawStream(device.index if device.index is not None
+                                               else torch.cuda.current_device())
 
 
 def _ptr(x: Optional[Tensor]) -> Optional[int]:
@@ -149,6 +166,7 @@ def _forward(q: Tensor, k: Tensor, v: Tensor, cu_seqlens_q: Optional[Tensor], cu
              seqused_k: Optional[Tensor], max_seqlen_q: int, max_seqlen_k: int, softmax_scale: float,
              window_left: int, window_right: int) -> tuple[Tensor, Tensor]:
     """O and the base-2 LSE (num_heads, rows), fp32 (flash_attn.py:353-373)."""
+    _same_device(q.device, k=k, v=v, cu_seqlens_q=cu_seqlens_q, cu_seqlens_k=cu_seqlens_k, seqused_k=seqused_k)
     varlen = cu_seqlens_q is not None
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
     cu_q, cu_k, seqused = _int32(cu_seqlens_q), _int32(cu_seqlens_k), _int32(seqused_k)
@@ -203,6 +221,8 @@ def _backward(dout: Tensor, q: Tensor, k: Tensor, v: Tensor, out: Tensor, lse: T
               max_seqlen_k: int, softmax_scale: float, window_left: int,
               window_right: int) -> tuple[Tensor, Tensor, Tensor]:
     """dQ, dK, dV (flash_attn.py:376-406)."""
+    _same_device(q.device, dout=dout, k=k, v=v, out=out, lse=lse, cu_seqlens_q=cu_seqlens_q,
+                 cu_seqlens_k=cu_seqlens_k)
     dout = _kernel_ready(dout)
     q, k, v, out = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v), _kernel_ready(out)
     cu_q, cu_k = _int32(cu_seqlens_q), _int32(cu_seqlens_k)
@@ -224,8 +244,19 @@ def _backward(dout: Tensor, q: Tensor, k: Tensor, v: Tensor, out: Tensor, lse: T
     return dq, dk, dv
 
 
+def _check_append(k_cache: Tensor, v_cache: Tensor, k: Tensor, v: Tensor, cache_seqlens: Tensor) -> None:
+    """The cache write copies 16-bit elements as they are: the new keys / values must have
+    the caches' dtype (the reference's index write raises on a mismatch too) and live on
+    the caches' GPU."""
+    if not (k.dtype == v.dtype == k_cache.dtype == v_cache.dtype):
+        raise TypeError(f"new keys/values ({k.dtype}, {v.dtype}) must match the caches' dtype "
+                        f"({k_cache.dtype}, {v_cache.dtype})")
+    _same_device(k_cache.device, v_cache=v_cache, k=k, v=v, cache_seqlens=cache_seqlens)
+
+
 def _kv_append(k_cache: Tensor, v_cache: Tensor, k: Tensor, v: Tensor, cache_seqlens: Tensor) -> None:
     """cache[b, cache_seqlens[b] + t] = new[b, t] (flash_attn.py:480-485)."""
+    _check_append(k_cache, v_cache, k, v, cache_seqlens)
     k, v = _kernel_ready(k), _kernel_ready(v)
     seqlens = _int32(cache_seqlens)
     p = _lib.KvAppendParams()
@@ -330,7 +361,8 @@ def flash_attn_func(
     q: Tensor, k: Tensor, v: Tensor, causal: bool = False, window_size: tuple[int, int] = (-1, -1),
     softmax_scale: float | None = None, *, return_softmax_lse: bool = False,
 ):
-    """q (batch, seqlen_q, heads, head_dim), k/v (batch, seqlen_k, kv_heads, head_dim)."""
+    """Attention over a dense batch: q is (B, Sq, Hq, D) and k, v are (B, Sk, Hkv, D) with Hq a
+    multiple of Hkv. Returns O shaped like q (and the base-2 LSE with return_softmax_lse)."""
     _check(q, k, v)
     q, k, v = (_last_dim_contiguous(x) for x in (q, k, v))
     scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(q.shape[-1])
@@ -343,9 +375,12 @@ def flash_attn_varlen_func(
     max_seqlen_k: int, causal: bool = False, window_size: tuple[int, int] = (-1, -1),
     softmax_scale: float | None = None, *, return_softmax_lse: bool = False,
 ):
-    """Packed q (total_q, heads, head_dim), k/v (total_k, kv_heads, head_dim); sequence b
-    spans rows cu_seqlens[b]:cu_seqlens[b + 1] (int32)."""
+    """Attention over packed documents: q is (Tq, Hq, D) and k, v are (Tk, Hkv, D); document b
+    owns query rows [cu_seqlens_q[b], cu_seqlens_q[b + 1]) and key rows likewise from
+    cu_seqlens_k (int32 offsets on q's GPU). max_seqlen_q / max_seqlen_k bound the longest
+    document and only size the launch grid."""
     _check(q, k, v)
+    _same_device(q.device, cu_seqlens_q=cu_seqlens_q, cu_seqlens_k=cu_seqlens_k)
     q, k, v = (_last_dim_contiguous(x) for x in (q, k, v))
     scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(q.shape[-1])
     out, lse = _FlashAttn.apply(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, scale,
@@ -358,13 +393,19 @@ def flash_attn_with_kvcache(
     cache_seqlens: Tensor, causal: bool = False, window_size: tuple[int, int] = (-1, -1),
     softmax_scale: float | None = None, return_softmax_lse: bool = False,
 ):
-    """Writes k/v (batch, new, kv_heads, head_dim) into the caches (batch, capacity,
-    kv_heads, head_dim) at cache_seqlens[b] onward, then attends q over each sequence's
-    cache_seqlens[b] + new keys. The caller advances cache_seqlens. Forward only.
-    Writes that would land at or beyond the capacity are dropped."""
+    """Decoding (or chunked prefill) against static caches k_cache / v_cache of shape
+    (B, capacity, Hkv, D). Given k and v of shape (B, new, Hkv, D), sequence b's rows are first
+    stored at cache positions cache_seqlens[b] + t; q then attends over the first
+    cache_seqlens[b] + new positions of its sequence. Advancing cache_seqlens is left to the
+    caller, and no gradient flows. A position at or past the capacity is not written (the
+    reference's index write would fault there) and the attended length is clipped to the
+    capacity."""
     _check(q, k_cache, v_cache)
     if k_cache.stride(-1) != 1 or v_cache.stride(-1) != 1:
         raise ValueError("the caches need a contiguous last dimension")
+    _same_device(q.device, cache_seqlens=cache_seqlens)
+    if k is not None and v is not None:
+        _check_append(k_cache, v_cache, k, v, cache_seqlens)
     q = _last_dim_contiguous(q)
     seqused = cache_seqlens.to(torch.int32)
     scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(q.shape[-1])

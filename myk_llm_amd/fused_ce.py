@@ -28,7 +28,7 @@ import torch
 from torch import Tensor
 
 from . import _lib
-from .flash_attn import _DeviceGuard, _dtype_code, _stream
+from .flash_attn import _DeviceGuard, _dtype_code, _same_device, _stream
 
 
 def _ce_rows(logits: Tensor, targets: Tensor, ce: Tensor, lse: Tensor, scale: float, z_coef: float,
@@ -48,40 +48,61 @@ def _accumulate_fp32(acc: Tensor, a: Tensor, b: Tensor) -> None:
     torch.ops.aten.addmm.dtype_out(acc, a, b, torch.float32, beta=1, alpha=1, out=acc)
 
 
-class _FusedLinearCE(torch.autograd.Function):
-    """fused_ce.py:70-108: gradients computed in the forward, scaled in the backward."""
+def _chunk_spans(n: int, size: int) -> list[tuple[int, int]]:
+    return [(lo, min(lo + size, n)) for lo in range(0, n, size)]
+
+
+def _loss_and_gradients(hidden: Tensor, weight: Tensor, targets: Tensor, scale: float, z_coef: float,
+                        ignore_index: int, chunk_size: int) -> tuple[Tensor, Tensor, Tensor]:
+    """One pass over the tokens in chunks. Returns (row_stats, d_hidden, d_weight):
+    row_stats[0] / row_stats[1] are every token's cross-entropy and natural-log LSE (fp32),
+    d_hidden (bf16) and d_weight (fp32) the gradients of the loss for an upstream gradient of 1.
+
+    Per chunk: the logits GEMM writes a (rows, vocab) bf16 block, the gfx950 row kernel turns
+    that block into d loss / d logits in place while producing the row statistics, and the
+    same block then feeds the two gradient GEMMs. d_weight is accumulated in fp32 by the
+    GEMM (beta = 1) so no partial sum is ever rounded to bf16."""
+    dev = hidden.device
+    tokens, width = hidden.shape
+    w16 = weight if weight.dtype == torch.bfloat16 else weight.to(torch.bfloat16)
+    row_stats = torch.empty((2, tokens), dtype=torch.float32, device=dev)
+    d_hidden = torch.empty((tokens, width), dtype=torch.bfloat16, device=dev)
+    d_weight = torch.zeros(weight.shape, dtype=torch.float32, device=dev)
+    tgt = targets if targets.dtype == torch.int64 else targets.to(torch.int64)
+    for lo, hi in _chunk_spans(tokens, chunk_size):
+        h16 = hidden[lo:hi]
+        if h16.dtype != torch.bfloat16:
+            h16 = h16.to(torch.bfloat16)
+        block = torch.mm(h16, w16.t())
+        _ce_rows(block, tgt[lo:hi], row_stats[0, lo:hi], row_stats[1, lo:hi], scale, z_coef, ignore_index)
+        torch.mm(block, w16, out=d_hidden[lo:hi])
+        _accumulate_fp32(d_weight, block.t(), h16)
+    return row_stats, d_hidden, d_weight
+
+
+class _LinearCrossEntropy(torch.autograd.Function):
+    """The loss and both gradients come out of the forward (the reference's scheme,
+    fused_ce.py:70-108): the backward only multiplies the stored gradients by the upstream
+    gradient of the loss and casts them to the parameters' dtypes."""
 
     @staticmethod
     def forward(ctx, hidden, weight, targets, normalizer, z_coef, ignore_index, chunk_size):  # pyright: ignore[reportIncompatibleMethodOverride]
-        num_tokens, hidden_size = hidden.shape
-        vocab_size = weight.shape[0]
         scale = 1.0 / normalizer
-        compute_dtype = torch.bfloat16  # GEMMs in bf16 (fp32 accumulate); softmax in fp32
-        weight_c = weight.to(compute_dtype)
-        grad_hidden = torch.empty(num_tokens, hidden_size, device=hidden.device, dtype=compute_dtype)
-        grad_weight = torch.zeros(vocab_size, hidden_size, device=hidden.device, dtype=torch.float32)
-        ce = torch.empty(num_tokens, device=hidden.device, dtype=torch.float32)
-        lse = torch.empty(num_tokens, device=hidden.device, dtype=torch.float32)
-        tgt = targets.to(torch.int64)
         with torch.autocast(device_type="cuda", enabled=False), _DeviceGuard(hidden.device):
-            for start in range(0, num_tokens, chunk_size):
-                end = min(start + chunk_size, num_tokens)
-                hidden_chunk = hidden[start:end].to(compute_dtype)
-                logits = hidden_chunk @ weight_c.t()
-                _ce_rows(logits, tgt[start:end], ce[start:end], lse[start:end], scale, z_coef, ignore_index)
-                torch.mm(logits, weight_c, out=grad_hidden[start:end])
-                _accumulate_fp32(grad_weight, logits.t(), hidden_chunk)
-        ctx.save_for_backward(grad_hidden, grad_weight)
-        ctx.hidden_dtype, ctx.weight_dtype = hidden.dtype, weight.dtype
-        ce_sum, z_sum = ce.sum(), lse.square().sum()
-        loss = (ce_sum + z_coef * z_sum) * scale
+            row_stats, d_hidden, d_weight = _loss_and_gradients(hidden, weight, targets, scale, z_coef,
+                                                                ignore_index, chunk_size)
+        ce_sum = row_stats[0].sum()
+        z_sum = torch.dot(row_stats[1], row_stats[1])
+        ctx.save_for_backward(d_hidden, d_weight)
+        ctx.grad_dtypes = (hidden.dtype, weight.dtype)
         ctx.mark_non_differentiable(ce_sum, z_sum)
-        return loss, ce_sum, z_sum
+        return torch.add(ce_sum, z_sum, alpha=z_coef) * scale, ce_sum, z_sum
 
     @staticmethod
-    def backward(ctx, grad_loss, _grad_ce, _grad_z):  # pyright: ignore[reportIncompatibleMethodOverride]
-        grad_hidden, grad_weight = ctx.saved_tensors
-        return ((grad_hidden * grad_loss).to(ctx.hidden_dtype), (grad_weight * grad_loss).to(ctx.weight_dtype),
+    def backward(ctx, upstream, _unused_ce, _unused_z):  # pyright: ignore[reportIncompatibleMethodOverride]
+        d_hidden, d_weight = ctx.saved_tensors
+        hidden_dtype, weight_dtype = ctx.grad_dtypes
+        return (d_hidden.mul(upstream).to(hidden_dtype), d_weight.mul(upstream).to(weight_dtype),
                 None, None, None, None, None)
 
 
@@ -93,8 +114,9 @@ def fused_linear_cross_entropy(hidden: Tensor, weight: Tensor, targets: Tensor, 
     with ignore_index marking unsupervised tokens."""
     if not hidden.is_cuda:
         raise RuntimeError("fused cross entropy is CUDA-only")
+    _same_device(hidden.device, weight=weight, targets=targets)
     if chunk_size <= 0:
         raise ValueError(f"chunk_size must be positive; got {chunk_size}")
-    result = _FusedLinearCE.apply(hidden.reshape(-1, hidden.size(-1)), weight, targets.reshape(-1),
-                                  float(normalizer), float(z_loss), ignore_index, chunk_size)
+    result = _LinearCrossEntropy.apply(hidden.reshape(-1, hidden.size(-1)), weight, targets.reshape(-1),
+                                       float(normalizer), float(z_loss), ignore_index, chunk_size)
     return cast(tuple[Tensor, Tensor, Tensor], result)

@@ -28,7 +28,7 @@ import torch
 from torch import Tensor
 
 from . import _lib
-from .flash_attn import _DeviceGuard, _stream
+from .flash_attn import _DeviceGuard, _same_device, _stream
 
 NS_COEFFICIENTS = (3.4445, -4.7750, 2.0315)  # ops/muon.py:25
 
@@ -58,6 +58,7 @@ def batched_syrk(x: Tensor, bias: Optional[Tensor] = None, alpha: float = 1.0, b
     if x.dim() != 3:
         raise ValueError(f"x must be (batch, m, k); got {tuple(x.shape)}")
     B, M, _ = x.shape
+    _same_device(x.device, bias=bias, out=out)
     if out is None:
         out = torch.empty((B, M, M), device=x.device, dtype=torch.bfloat16)
     if out.shape != (B, M, M) or out.dtype != torch.bfloat16:

@@ -28,17 +28,19 @@ def storage_ulp(x, dtype):
 
 def assert_north_star(actual, expected, max_abs=2e-2, mean_abs=2e-3, what=""):
     """The north-star bounds against the fp32 reference: mean-abs <= 2e-3, and max-abs <= 2e-2
-    beyond one storage ulp of each element. A 16-bit result cannot be closer to an fp32 value
-    than its own rounding: for |x| in [4, 8) a bf16 ulp is 2^-5 = 0.031 > 2e-2, so an
-    absolute 2e-2 alone is unreachable for large gradients even by the fp32 reference
-    rounded to bf16; the ulp term admits exactly that representation error."""
+    beyond the storage floor of each element. A 16-bit result cannot be closer to an fp32 value
+    than its own rounding, which is at most half an ulp (round to nearest): for |x| in [8, 16)
+    a bf16 ulp is 2^-4, so even the fp32 reference rounded to bf16 misses it by up to
+    2^-5 = 0.031 > 2e-2. The half-ulp term admits exactly that representation error and
+    nothing more. Returns (max-abs, mean-abs, max-abs beyond the floor)."""
     exp = expected.float().to(actual.device)
     d = (actual.float() - exp).abs()
     mx, mn = d.max().item(), d.mean().item()
-    excess = (d - storage_ulp(exp, actual.dtype)).max().item()
+    excess = (d - 0.5 * storage_ulp(exp, actual.dtype)).max().item()
     assert mn <= mean_abs and excess <= max_abs, (
-        f"{what}: max-abs {mx:.3e}, beyond one storage ulp {excess:.3e} (<= {max_abs}), "
+        f"{what}: max-abs {mx:.3e}, beyond half a storage ulp {excess:.3e} (<= {max_abs}), "
         f"mean-abs {mn:.3e} (<= {mean_abs})")
+    return mx, mn, excess
 
 
 def assert_lse(actual, expected, tol=1e-3, what="lse"):
@@ -60,3 +62,16 @@ def random_qkv(batch, seqlen_q, seqlen_k, heads, kv_heads, head_dim, packed=Fals
         return torch.randn(*shape).to(dtype).to(device).requires_grad_(requires_grad)
 
     return make(*lead_q, heads, head_dim), make(*lead_k, kv_heads, head_dim), make(*lead_k, kv_heads, head_dim)
+
+
+def record_parity(config, name, **fields):
+    """Appends one JSON line of measured errors to the file named by MYKFA_PARITY_LOG (nothing
+    when unset), so a run's raw parity numbers can be kept beside its log."""
+    import json
+    import os
+
+    path = os.environ.get("MYKFA_PARITY_LOG")
+    if not path:
+        return
+    with open(path, "a") as f:
+        f.write(json.dumps({"config": config, "tensor": name, **fields}) + "\n")

@@ -92,3 +92,24 @@ def test_custom_op_shape_functions():
         assert lse.shape == (8, 11)
         dq, dk, dv = torch.ops.mykfa.bwd(q, q, k, k, q, torch.empty(8, 14), None, None, 7, 9, 0.125, 1 << 30, 0)
         assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == k.shape
+
+
+def test_device_and_dtype_guards_raise_on_the_host():
+    """The guards run before any launch and need no GPU: a tensor on another device, or new
+    keys of another dtype than the caches, raise."""
+    from myk_llm_amd.flash_attn import _check_append, _same_device
+
+    gpu = torch.device("cuda", 0)
+    x = torch.zeros(4)
+    _same_device(gpu, a=None)
+    with pytest.raises(RuntimeError, match="same GPU"):
+        _same_device(gpu, cu_seqlens_q=x)
+    with pytest.raises(RuntimeError, match="cache_seqlens"):
+        _same_device(gpu, k=None, cache_seqlens=x.int())
+    cache = torch.zeros(1, 8, 2, 16, dtype=torch.bfloat16)
+    new = torch.zeros(1, 1, 2, 16, dtype=torch.bfloat16)
+    _check_append(cache, cache, new, new, torch.zeros(1, dtype=torch.int32))  # all on the host: consistent
+    with pytest.raises(TypeError):
+        _check_append(cache, cache, new.half(), new.half(), torch.zeros(1, dtype=torch.int32))
+    with pytest.raises(TypeError):
+        _check_append(cache, cache, new.float(), new, torch.zeros(1, dtype=torch.int32))

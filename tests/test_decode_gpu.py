@@ -22,23 +22,24 @@ def _say(*a):
     sys.stdout.flush()
 
 
-def _make(batch, cap, lens, nq, heads, kv_heads, d, seed=0):
+def _make(batch, cap, lens, nq, heads, kv_heads, d, seed=0, dtype=torch.bfloat16):
     g = torch.Generator().manual_seed(seed)
-    kc = torch.randn(batch, cap, kv_heads, d, generator=g).to(torch.bfloat16)
-    vc = torch.randn(batch, cap, kv_heads, d, generator=g).to(torch.bfloat16)
-    q = torch.randn(batch, nq, heads, d, generator=g).to(torch.bfloat16)
-    kn = torch.randn(batch, nq, kv_heads, d, generator=g).to(torch.bfloat16)
-    vn = torch.randn(batch, nq, kv_heads, d, generator=g).to(torch.bfloat16)
+    kc = torch.randn(batch, cap, kv_heads, d, generator=g).to(dtype)
+    vc = torch.randn(batch, cap, kv_heads, d, generator=g).to(dtype)
+    q = torch.randn(batch, nq, heads, d, generator=g).to(dtype)
+    kn = torch.randn(batch, nq, kv_heads, d, generator=g).to(dtype)
+    vn = torch.randn(batch, nq, kv_heads, d, generator=g).to(dtype)
     return q, kc, vc, kn, vn, torch.tensor(lens, dtype=torch.int32)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("nq", [1, 2, 4, 16])
 @pytest.mark.parametrize("heads, kv_heads", [(16, 4), (8, 8), (8, 1)])
 @pytest.mark.parametrize("window", [(-1, -1), (100, 0)])
-def test_decode_matches_oracle(nq, heads, kv_heads, window):
-    _say(f"decode nq={nq} H={heads}/{kv_heads} window={window}")
+def test_decode_matches_oracle(nq, heads, kv_heads, window, dtype):
+    _say(f"decode nq={nq} H={heads}/{kv_heads} window={window} {dtype}")
     lens = [0, 1, 31, 32, 33, 500, 1000, 2047]
-    q, kc, vc, kn, vn, cl = _make(len(lens), 2100, lens, nq, heads, kv_heads, 64)
+    q, kc, vc, kn, vn, cl = _make(len(lens), 2100, lens, nq, heads, kv_heads, 64, dtype=dtype)
     exp, exp_lse, ekc, evc = kvcache_reference(q.float(), kc.float(), vc.float(), kn.float(), vn.float(), cl, True,
                                                window)
     kcg, vcg = kc.cuda(), vc.cuda()
@@ -50,11 +51,12 @@ def test_decode_matches_oracle(nq, heads, kv_heads, window):
     assert_lse(lse, exp_lse)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("d", [16, 32, 64, 128, 256])
-def test_decode_head_dims(d):
-    _say(f"decode D={d}")
+def test_decode_head_dims(d, dtype):
+    _say(f"decode D={d} {dtype}")
     lens = [7, 300, 129]
-    q, kc, vc, kn, vn, cl = _make(3, 400, lens, 4, 8, 2, d, seed=1)
+    q, kc, vc, kn, vn, cl = _make(3, 400, lens, 4, 8, 2, d, seed=1, dtype=dtype)
     exp, exp_lse, _, _ = kvcache_reference(q.float(), kc.float(), vc.float(), kn.float(), vn.float(), cl, True,
                                            (-1, -1))
     out, lse = flash_attn_with_kvcache(q.cuda(), kc.cuda(), vc.cuda(), kn.cuda(), vn.cuda(), cache_seqlens=cl.cuda(),
@@ -181,6 +183,45 @@ def test_decode_counts_preappended_keys():
                            n_new=kn.shape[1])
     assert_close(out, exp)
     assert_lse(lse, exp_lse)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_append_then_attend_path(dtype):
+    """More than 16 new queries take the separate append kernel, then the prefill forward over
+    cache_seqlens + new keys (flash_attn.py:480-488); the cache write is bit-exact."""
+    _say(f"append path {dtype}")
+    lens = [0, 40, 300]
+    q, kc, vc, kn, vn, cl = _make(len(lens), 512, lens, 24, 8, 2, 64, seed=7, dtype=dtype)
+    exp, exp_lse, ekc, evc = kvcache_reference(q.float(), kc.float(), vc.float(), kn.float(), vn.float(), cl, True,
+                                               (-1, -1))
+    kcg, vcg = kc.cuda(), vc.cuda()
+    out, lse = flash_attn_with_kvcache(q.cuda(), kcg, vcg, kn.cuda(), vn.cuda(), cache_seqlens=cl.cuda(),
+                                       causal=True, return_softmax_lse=True)
+    assert torch.equal(kcg.cpu().float(), ekc) and torch.equal(vcg.cpu().float(), evc)
+    assert_close(out, exp)
+    assert_lse(lse, exp_lse)
+
+
+def test_mismatched_new_keys_raise_before_any_launch():
+    """New keys/values must share the caches' dtype and GPU, and cache_seqlens must be on the
+    GPU: each mismatch raises and leaves the caches untouched (on both the fused decode path
+    and the separate append path)."""
+    q, kc, vc, kn, vn, cl = _make(2, 64, [3, 5], 1, 4, 2, 64)
+    q, kc, vc, cl = q.cuda(), kc.cuda(), vc.cuda(), cl.cuda()
+    kc0 = kc.clone()
+    for nq in (1, 20):
+        qq = q.expand(2, nq, 4, 64).contiguous()
+        knn, vnn = kn.expand(2, nq, 2, 64).contiguous(), vn.expand(2, nq, 2, 64).contiguous()
+        with pytest.raises(TypeError):
+            flash_attn_with_kvcache(qq, kc, vc, knn.cuda().half(), vnn.cuda().half(), cache_seqlens=cl, causal=True)
+        with pytest.raises(TypeError):
+            flash_attn_with_kvcache(qq, kc, vc, knn.cuda().float(), vnn.cuda().float(), cache_seqlens=cl, causal=True)
+        with pytest.raises(RuntimeError):
+            flash_attn_with_kvcache(qq, kc, vc, knn, vnn, cache_seqlens=cl, causal=True)  # new keys on the host
+        with pytest.raises(RuntimeError):
+            flash_attn_with_kvcache(qq, kc, vc, knn.cuda(), vnn.cuda(), cache_seqlens=cl.cpu(), causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(kc, kc0)
 
 
 def test_new_keys_of_the_wrong_shape_raise():

@@ -181,6 +181,33 @@ def test_fp16_inputs():
         assert_close(grad, eg)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("seqlen_q", [1, 4, 16])
+def test_short_queries_take_the_decode_kernels(dtype, seqlen_q):
+    """flash_attn_func with at most 16 queries runs the split-K decode kernels (the reference's
+    decode config, flash_attn.py:364), in both input types."""
+    _say(f"short queries Lq={seqlen_q} {dtype}")
+    torch.manual_seed(7)
+    q, k, v = random_qkv(3, seqlen_q, 700, 8, 2, 64, dtype=dtype, requires_grad=False)
+    out, lse = flash_attn_func(q, k, v, causal=True, return_softmax_lse=True)
+    assert out.dtype == dtype
+    qc, kc, vc = _cpu(q, k, v)
+    expected, expected_lse = reference_with_lse(qc, kc, vc, True, (-1, -1))
+    assert_close(out, expected)
+    assert_lse(lse, expected_lse)
+
+
+def test_auxiliary_tensors_on_the_host_are_rejected():
+    """cu_seqlens on the host would hand the kernel a host pointer: rejected before launch, like
+    the reference (a device mismatch)."""
+    q, k, v = random_qkv(1, 64, 64, 4, 2, 64, packed=True, requires_grad=False)
+    cu = torch.tensor([0, 30, 64], dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="same GPU"):
+        flash_attn_varlen_func(q, k, v, cu, cu.cuda(), 34, 34, causal=True)
+    with pytest.raises(RuntimeError, match="same GPU"):
+        flash_attn_varlen_func(q, k, v, cu.cuda(), cu, 34, 34, causal=True)
+
+
 def test_strided_views_of_a_fused_projection():
     """q/k/v as views of one fused qkv tensor (mixers.py:81-84): non-contiguous head strides."""
     torch.manual_seed(3)
