@@ -343,6 +343,22 @@ int mykfa_decode_merge(const mykfa_decode_params* p, const void* workspace,
 int mykfa_decode(const mykfa_decode_params* p, void* workspace, size_t workspace_bytes,
                  mykfa_stream_t stream);
 
+/* Size of the static scratch array behind mykfa_decode_noalloc (per GPU, held until the
+ * process ends). */
+#define MYKFA_DECODE_SCRATCH_BYTES ((size_t)16 << 20)
+/* Allocation-free split-K decode + merge: no counterpart in the reference. For callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). Same parameters and results as mykfa_decode, but the split partials
+ * live in a file-scope device array of MYKFA_DECODE_SCRATCH_BYTES (16 MiB) instead of a
+ * caller workspace; nothing is allocated or freed. With num_splits = 0 the library's split
+ * count is cut to what the scratch holds; an explicit num_splits whose partials exceed it is
+ * rejected (MYKFA_ERR_WORKSPACE). Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (concurrent streams) race and must be serialized by the caller. Nothing
+ * in the array needs to start at zero (each call writes every partial its merge reads). The
+ * first call on each device resolves the array's address (hipGetSymbolAddress): make one call
+ * outside graph capture before capturing. */
+int mykfa_decode_noalloc(const mykfa_decode_params* p, mykfa_stream_t stream);
+
 /* ---- KV append ------------------------------------------------------------------------ */
 /* Replaces the advanced-index cache writes of flash_attn_with_kvcache
  * (flash_attn.py:480-485); graph-capturable (no host sync). */

@@ -19,6 +19,7 @@ ERR_INVALID = 1
 ERR_UNSUPPORTED = 2
 ERR_LAUNCH = 3
 ERR_WORKSPACE = 4
+DECODE_SCRATCH_BYTES = 16 << 20  # MYKFA_DECODE_SCRATCH_BYTES
 
 DTYPE_BF16 = 0
 DTYPE_FP16 = 1
@@ -154,6 +155,7 @@ SIGNATURES = {
     "mykfa_decode_splitk": (ctypes.c_int, [ctypes.POINTER(DecodeParams), _ptr, ctypes.c_size_t, _ptr]),
     "mykfa_decode_merge": (ctypes.c_int, [ctypes.POINTER(DecodeParams), _ptr, ctypes.c_size_t, _ptr]),
     "mykfa_decode": (ctypes.c_int, [ctypes.POINTER(DecodeParams), _ptr, ctypes.c_size_t, _ptr]),
+    "mykfa_decode_noalloc": (ctypes.c_int, [ctypes.POINTER(DecodeParams), _ptr]),
     "mykfa_kv_append": (ctypes.c_int, [ctypes.POINTER(KvAppendParams), _ptr]),
     "mykfa_sizeof_qk_prologue_params": (ctypes.c_size_t, []),
     "mykfa_sizeof_qk_prologue_bwd_params": (ctypes.c_size_t, []),

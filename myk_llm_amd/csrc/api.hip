@@ -418,6 +418,41 @@ int mykfa_decode(const mykfa_decode_params* p, void* workspace, size_t workspace
     return mykfa_decode_merge(p, workspace, workspace_bytes, stream);
 }
 
+int mykfa_decode_noalloc(const mykfa_decode_params* p, mykfa_stream_t stream) {
+    int rc = check_decode(p);
+    if (rc) return rc;
+    if (p->fwd.batch == 0 || p->fwd.max_seqlen_q == 0) return ok();
+    const size_t cap = MYKFA_DECODE_SCRATCH_BYTES;
+    const size_t per_split = mykfa::decode_workspace_bytes(p->fwd.batch, p->fwd.num_heads, p->fwd.max_seqlen_q,
+                                                           p->fwd.head_dim, 2) / 2;
+    int splits = choose_splits(p);
+    if (p->num_splits > 0) {
+        const size_t need = mykfa::decode_workspace_bytes(p->fwd.batch, p->fwd.num_heads, p->fwd.max_seqlen_q,
+                                                          p->fwd.head_dim, splits);
+        if (need > cap)
+            return fail(MYKFA_ERR_WORKSPACE,
+                        "mykfa_decode_noalloc: %d splits need %zu bytes of scratch, beyond its fixed %zu bytes "
+                        "(use fewer splits, num_splits = 0, or mykfa_decode with a workspace)",
+                        splits, need, cap);
+    } else if (per_split > 0 && (size_t)splits * per_split > cap) {
+        // The library's own choice is cut to what the scratch holds (off multiples of the 8 XCDs).
+        splits = (int)(cap / per_split);
+        if (splits > 1 && splits % 8 == 0) --splits;
+        if (splits < 1) splits = 1;
+    }
+    void* ws = nullptr;
+    if (splits > 1) {
+        const hipError_t e = mykfa::decode_scratch(&ws);
+        if (e != hipSuccess)
+            return fail(MYKFA_ERR_LAUNCH, "mykfa_decode_noalloc: scratch address: %s", hipGetErrorString(e));
+    }
+    mykfa_decode_params q = *p;
+    q.num_splits = splits;
+    rc = launched(mykfa::launch_decode_splitk(q, splits, ws, as_stream(stream)), "mykfa_decode_noalloc");
+    if (rc || splits == 1) return rc;
+    return launched(mykfa::launch_decode_merge(q, splits, ws, as_stream(stream)), "mykfa_decode_noalloc");
+}
+
 int mykfa_kv_append(const mykfa_kv_append_params* p, mykfa_stream_t stream) {
     int rc = check_append(p);
     if (rc) return rc;

@@ -20,10 +20,19 @@
 // O^T += V^T P^T. A wave then
 // writes either the final O/LSE (one split) or an fp32 partial (O, lse) that the merge kernel
 // combines: lse = log2(sum_s 2^lse_s), O = sum_s 2^(lse_s - lse) O_s.
+#include <mutex>
+
 #include "common.h"
 #include "kernels.h"
 
 namespace mykfa {
+
+// Split-K workspace of the allocation-free decode entry point (mykfa_decode_noalloc): a
+// file-scope device array, one copy per GPU the library runs on, held until the process ends.
+// Host code never uses this name as an address (in host code it is only a stand-in for the
+// device symbol): decode_scratch() resolves each device's copy once with hipGetSymbolAddress
+// and every launch passes that pointer.
+static __device__ __align__(256) unsigned char scratch[MYKFA_DECODE_SCRATCH_BYTES];
 
 namespace {
 
@@ -540,6 +549,27 @@ hipError_t launch_decode_merge(const mykfa_decode_params& p, int num_splits, con
     DecodeArgs a = make_args(p, num_splits, const_cast<void*>(ws));
     if (p.fwd.dtype == MYKFA_BF16) return merge_dtype<BF16>(a, p.fwd.head_dim, stream);
     return merge_dtype<FP16>(a, p.fwd.head_dim, stream);
+}
+
+hipError_t decode_scratch(void** ptr) {
+    // Device addresses of `scratch`, resolved on the first call made with each device current.
+    constexpr int kMaxDevices = 64;
+    static std::mutex mu;
+    static void* resolved[kMaxDevices] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(mu);
+    if (resolved[dev] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (p == nullptr) return hipErrorInvalidSymbol;
+        resolved[dev] = p;
+    }
+    *ptr = resolved[dev];
+    return hipSuccess;
 }
 
 hipError_t launch_kv_append(const mykfa_kv_append_params& p, hipStream_t stream) {

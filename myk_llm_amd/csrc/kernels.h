@@ -21,6 +21,9 @@ int decode_default_splits(int batch, int num_heads, int num_kv_heads, int seqlen
 hipError_t launch_decode_splitk(const mykfa_decode_params& p, int num_splits, void* ws, hipStream_t stream);
 hipError_t launch_decode_merge(const mykfa_decode_params& p, int num_splits, const void* ws,
                                hipStream_t stream);
+// This device's copy of the allocation-free decode's static scratch array (resolved once per
+// device; MYKFA_DECODE_SCRATCH_BYTES long).
+hipError_t decode_scratch(void** ptr);
 
 hipError_t launch_kv_append(const mykfa_kv_append_params& p, hipStream_t stream);
 
