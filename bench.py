@@ -6,8 +6,9 @@ One "step" is one pass of the hot path over one batch of synthetic input. The he
 workload is BASELINE config 2 (GQA varlen causal, 8 packed documents, 8248 tokens, Hq=16,
 Hkv=4, D=64, bf16), run as forward + backward through the public API (the north-star
 target is fwd+bwd on this 8K-token GQA varlen shape). Prefill steps are timed as the
-reference times them (scripts/benchmark_attention.py:31-40): eager public-API calls, HIP
-events around the repeats; the host enqueues a step (~160 us) faster than the GPU runs it,
+reference times them (scripts/benchmark_attention.py:31-40): eager public-API calls back to
+back with HIP events around them, here split into 5 consecutive blocks and reported as the
+median block's time per step; the host enqueues a step (~160 us) faster than the GPU runs it,
 so the GPU never waits. --graph replays a captured HIP graph instead (ROCm 7 adds ~7 us
 between graph kernel nodes, which back-to-back eager launches do not). Decode steps are
 graph replays, as in the reference's scripts/benchmark_decode.py:122-157, which captures a
@@ -25,7 +26,8 @@ Printed: ONE JSON line with the headline value, a "roofline" object for the step
 dominant kernel (its algorithmic FLOPs / its average duration measured with HIP events on
 its launch stream), a "cpu_baseline" object (the oracle's fp32 CPU attention on a bounded
 sample, timed on this host's cores), and a "configs" object with every other BASELINE
-config (fwd / fwd+bwd TFLOP/s, decode GB/s, fractions of peak).
+config (fwd / fwd+bwd TFLOP/s with a roofline object per fwd+bwd config, decode GB/s,
+fractions of peak) and the reference benchmark's six shapes beside its published times.
 """
 
 from __future__ import annotations
@@ -34,6 +36,7 @@ import argparse
 import ctypes
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -67,19 +70,25 @@ def settle(fn, seconds: float = 0.3) -> None:
         torch.cuda.synchronize()
 
 
-def time_events(fn, reps: int, warmup: int = 2) -> float:
-    """Average ms per call of fn (launches on torch's current stream), HIP events around reps,
-    after `warmup` untimed calls and a settle() of the clocks."""
+def time_events(fn, reps: int, warmup: int = 2, blocks: int = 5) -> float:
+    """ms per call of fn (launches on torch's current stream): after `warmup` untimed calls and
+    a settle() of the clocks, exactly `reps` calls back to back, split into `blocks`
+    consecutive blocks with a HIP event between blocks (no synchronization inside the timed
+    region); the median over the blocks of each block's time per call."""
     for _ in range(warmup):
         fn()
     settle(fn)
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(reps):
-        fn()
-    end.record()
+    nb = max(1, min(blocks, reps))
+    sizes = [reps // nb + (1 if i < reps % nb else 0) for i in range(nb)]
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(nb + 1)]
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / reps
+    events[0].record()
+    for i, n in enumerate(sizes):
+        for _ in range(n):
+            fn()
+        events[i + 1].record()
+    torch.cuda.synchronize()
+    return statistics.median(events[i].elapsed_time(events[i + 1]) / sizes[i] for i in range(nb))
 
 
 def capture(fn, warmup: int = 3):
@@ -129,6 +138,13 @@ class KernelCalls:
             p.dv_batch_stride, p.dv_token_stride, p.dv_head_stride = fa._strides(self.dv)
             self.bp = p
             self.keep.append(dout)
+            # The stored-dS schedule that the autograd backward takes for this shape (head_dim
+            # 128 within the default budget): delta, dK/dV storing dS, dQ from dS.
+            per = self.L.mykfa_bwd_workspace_per_kv_head(ctypes.byref(p))
+            heads = k.shape[-2]
+            self.ws = None
+            if per and heads * per <= fa._ds_budget_bytes():
+                self.ws = torch.empty(heads * per, dtype=torch.uint8, device=q.device)
 
     def fwd(self):
         _lib.check(self.L.mykfa_fwd(ctypes.byref(self.fp), self.stream))
@@ -138,6 +154,15 @@ class KernelCalls:
 
     def dq_(self):
         _lib.check(self.L.mykfa_bwd_dq(ctypes.byref(self.bp), self.stream))
+
+    def delta_(self):
+        _lib.check(self.L.mykfa_bwd_preprocess(ctypes.byref(self.bp), self.stream))
+
+    def dkdv_ds(self):
+        _lib.check(self.L.mykfa_bwd_dkdv_ws(ctypes.byref(self.bp), self.ws.data_ptr(), self.ws.numel(), self.stream))
+
+    def dq_ds(self):
+        _lib.check(self.L.mykfa_bwd_dq_ws(ctypes.byref(self.bp), self.ws.data_ptr(), self.ws.numel(), self.stream))
 
 
 class DecodeCalls:
@@ -211,15 +236,81 @@ def measure_prefill(w, steps: int, warmup: int, backward: bool, use_graph: bool 
                      inp["dout"] if backward else None)
     reps = max(steps, 10)
     kern = {"fwd": time_events(kc.fwd, reps)}
-    if backward:
-        # The step's backward is dQ (which also computes delta = rowsum(dO * O)) then dK/dV.
+    if backward and kc.ws is not None:
+        # Stored-dS backward: delta, dK/dV (also storing dS), dQ from dS.
+        kern["bwd_delta"] = time_events(kc.delta_, reps)
+        kern["bwd_dkdv"] = time_events(kc.dkdv_ds, reps)
+        kern["bwd_dq"] = time_events(kc.dq_ds, reps)
+    elif backward:
+        # Recomputing backward: dQ (which also computes delta = rowsum(dO * O)) then dK/dV.
         kern["bwd_dq"] = time_events(kc.dq_, reps)
         kern["bwd_dkdv"] = time_events(kc.dkdv, reps)
     # Algorithmic FLOPs per launch (convention split: fwd = 2 products; of the 5 backward
-    # products, dK/dV's kernel owns S, dP, dV, dK = 2.0 F_fwd and dQ's owns dQ = 0.5 F_fwd).
+    # products, dK/dV's kernel owns S, dP, dV, dK = 2.0 F_fwd and dQ's owns dQ = 0.5 F_fwd;
+    # delta is HBM-bound streaming, no credited FLOPs).
     algo = {"fwd": w.fwd_flops, "bwd_dkdv": 2.0 * w.fwd_flops, "bwd_dq": 0.5 * w.fwd_flops}
     del inp, step, kc
     return ms, flops, kern, algo
+
+
+def roofline_of(kern, algo, profile=None):
+    """The roofline object of the dominant kernel among those with credited FLOPs: its
+    algorithmic FLOPs / its duration, against the bf16 dense peak; traffic from the committed
+    copy-calibrated counter summary of `profile`, when there is one."""
+    dom = max((k for k in kern if algo.get(k, 0) > 0), key=lambda k: kern[k])
+    achieved = algo[dom] / (kern[dom] * 1e-3) / 1e12
+    return {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2), "peak": BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
+            "traffic": profiled_traffic(dom, profile) if profile else None, "kernel_ms": round(kern[dom], 5)}
+
+
+# The reference's own benchmark shapes (scripts/benchmark_attention.py:21-29) and its published
+# times, fwd / fwd+bwd in ms, of its Triton kernels on its development GPU (an sm_120 part;
+# notes/flash-attn.md:62-67): context for the MI355X numbers, not a target.
+REFERENCE_SHAPES = [
+    # (batch, seq_len, heads, kv_heads, head_dim, window or None, documents or None, published)
+    (8, 2048, 8, 2, 128, None, None, (0.385, 1.706)),
+    (8, 2048, 8, 2, 128, 512, None, (0.198, 0.783)),
+    (8, 2048, 8, 2, 128, None, [300, 700, 48, 1000], (0.199, 0.804)),
+    (2, 8192, 8, 2, 128, None, None, (1.387, 6.035)),
+    (16, 1024, 4, 4, 64, None, None, (0.058, 0.236)),
+    (16, 1024, 4, 4, 64, 256, None, (0.029, 0.113)),
+]
+
+
+def measure_reference_shapes(reps: int = 30):
+    """Forward and forward + backward at the reference benchmark's shapes, set up as it sets
+    them up (scripts/benchmark_attention.py:44-62: N(0,1) bf16 inputs, windows as
+    (window - 1, 0), documents packed with cu_seqlens, the backward as autograd.grad of the
+    forward), timed by time_events. FLOPs: 4 * visible pairs * heads * head_dim, x 3.5 for
+    forward + backward (:49-50, :86)."""
+    out = []
+    g = torch.Generator(device="cuda").manual_seed(0)
+    for batch, seq, h, hk, d, window, docs, published in REFERENCE_SHAPES:
+        make = lambda n: torch.randn(batch, seq, n, d, device="cuda", generator=g).to(torch.bfloat16)
+        q, k, v, do = make(h), make(hk), make(hk), make(h)
+        lengths = docs or [seq]
+        pairs = batch * sum(min(i + 1, window or seq) for n in lengths for i in range(n))
+        flops = 4.0 * pairs * h * d
+        ws = (window - 1, 0) if window else (-1, -1)
+        if docs is None:
+            inputs = tuple(x.requires_grad_() for x in (q, k, v))
+            grad = do
+            fwd = lambda: flash_attn_func(*inputs, causal=True, window_size=ws)
+        else:
+            cu = torch.tensor([0] + list(torch.tensor(docs * batch).cumsum(0)), dtype=torch.int32, device="cuda")
+            inputs = tuple(x.flatten(0, 1).requires_grad_() for x in (q, k, v))
+            grad = do.flatten(0, 1)
+            fwd = lambda: flash_attn_varlen_func(*inputs, cu, cu, seq, seq, causal=True, window_size=ws)
+        ms_f = time_events(fwd, reps, warmup=3)
+        ms_b = time_events(lambda: torch.autograd.grad(fwd(), inputs, grad), reps, warmup=3)
+        out.append({"shape": {"batch": batch, "seq_len": seq, "heads": h, "kv_heads": hk, "head_dim": d,
+                              "window": window, "documents": docs},
+                    "fwd_ms": round(ms_f, 4), "fwd_TFLOP/s": round(flops / (ms_f * 1e-3) / 1e12, 1),
+                    "fwdbwd_ms": round(ms_b, 4), "fwdbwd_TFLOP/s": round(3.5 * flops / (ms_b * 1e-3) / 1e12, 1),
+                    "reference_published_ms": {"fwd": published[0], "fwdbwd": published[1]}})
+        del q, k, v, do, inputs, grad
+    return out
 
 
 DECODE_LAYERS = 4
@@ -621,8 +712,7 @@ def main():
     torch.cuda.synchronize()
     ms, flops, kern, algo = measure_prefill(w, args.steps, args.warmup, backward=True, use_graph=args.graph)
     value = flops / (ms * 1e-3) / 1e12
-    dom = max((k for k in kern if algo.get(k, 0) > 0), key=lambda k: kern[k])
-    achieved = algo[dom] / (kern[dom] * 1e-3) / 1e12
+    roof = roofline_of(kern, algo, f"{args.workload}_fwdbwd")
     log(f"  {ms:.4f} ms/step, {value:.1f} TFLOP/s; kernels (ms): " + ", ".join(f"{k}={v:.4f}" for k, v in kern.items()))
     configs = {}
     if not args.quick:
@@ -630,12 +720,14 @@ def main():
             wk = W[name]
             for bwd in ((False, True) if name != "cfg2" else (False,)):
                 log(f"config {wk.name} {'fwd+bwd' if bwd else 'fwd'}")
-                m, f, kk, _ = measure_prefill(wk, max(10, args.steps // 2), 3, backward=bwd, use_graph=args.graph)
+                m, f, kk, algo_k = measure_prefill(wk, max(10, args.steps // 2), 3, backward=bwd, use_graph=args.graph)
                 t = f / (m * 1e-3) / 1e12
-                configs[f"{name}_{'fwdbwd' if bwd else 'fwd'}"] = {
+                key = f"{name}_{'fwdbwd' if bwd else 'fwd'}"
+                configs[key] = {
                     "workload": wk.name, "ms": round(m, 5), "TFLOP/s": round(t, 2),
                     "frac_of_bf16_peak": round(t / BF16_PEAK_TFLOPS, 4),
-                    "kernel_ms": {k: round(v, 5) for k, v in kk.items()}}
+                    "kernel_ms": {k: round(v, 5) for k, v in kk.items()},
+                    "roofline": roofline_of(kk, algo_k, key if bwd else None)}
                 log(f"  {m:.4f} ms, {t:.1f} TFLOP/s")
         for name in ("cfg5", "cfg5_mtp"):
             wk = W[name]
@@ -661,6 +753,11 @@ def main():
         log("Muon batched SYRK and Newton-Schulz")
         configs["muon_syrk"] = measure_syrk(args.steps)
         log("  " + json.dumps(configs["muon_syrk"]))
+        log("the reference benchmark's shapes")
+        configs["reference_shapes"] = measure_reference_shapes()
+        for r in configs["reference_shapes"]:
+            log(f"  {r['shape']}: fwd {r['fwd_ms']} ms {r['fwd_TFLOP/s']} TFLOP/s, fwd+bwd {r['fwdbwd_ms']} ms "
+                f"{r['fwdbwd_TFLOP/s']} TFLOP/s (reference, its GPU: {r['reference_published_ms']})")
         log("attention-block prologue / epilogue at the cfg3 shape")
         configs["block_io_cfg3"] = measure_block_io(W["cfg3"], args.steps)
         log("  " + json.dumps(configs["block_io_cfg3"]))
@@ -686,10 +783,7 @@ def main():
                    "heads": w.heads, "kv_heads": w.kv_heads, "head_dim": w.head_dim,
                    "timing": "hipgraph replay" if args.graph else "eager calls, HIP events", "parallelism": "none (1 GPU)"},
         "frac_of_bf16_peak": round(value / BF16_PEAK_TFLOPS, 4),
-        "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2), "peak": BF16_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
-                     "traffic": profiled_traffic(dom),
-                     "kernel_ms": round(kern[dom], 5)},
+        "roofline": roof,
         "kernels_ms": {k: round(v, 5) for k, v in kern.items()},
         "cpu_baseline": cpu,
         "configs": configs,

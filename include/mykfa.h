@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define MYKFA_ABI_VERSION 6
+#define MYKFA_ABI_VERSION 7
 #define MYKFA_UNBOUNDED (1 << 30) /* flash_attn.py:32 (_UNBOUNDED) */
 
 /* Status codes. */
@@ -322,6 +322,23 @@ int mykfa_bwd_dkdv(const mykfa_bwd_params* p, mykfa_stream_t stream);
 int mykfa_bwd_dq(const mykfa_bwd_params* p, mykfa_stream_t stream);
 /* dQ (with delta) then dK/dV in stream order (replaces _backward, flash_attn.py:376-406). */
 int mykfa_bwd(const mykfa_bwd_params* p, mykfa_stream_t stream);
+/* Backward through stored dS (replaces _backward, flash_attn.py:376-406, like mykfa_bwd):
+ * delta, then dK/dV, which also stores every 32 x 32 block of dS (rounded to the input type,
+ * as the reference rounds it before its dQ product, flash_attn.py:177) into the workspace,
+ * then dQ = scale * dS K from those blocks: five products per (query tile, key block) pair
+ * instead of seven. Deterministic, no atomics. The workspace holds the dS of whole KV heads:
+ * mykfa_bwd_workspace_per_kv_head bytes each (0 when head_dim is not 128, where the trade does
+ * not pay); with workspace_bytes >= n times that, KV heads are processed in passes of up to n.
+ * With less than one KV head's worth this is mykfa_bwd (dQ recomputes S and dP). */
+size_t mykfa_bwd_workspace_per_kv_head(const mykfa_bwd_params* p);
+int mykfa_bwd_ws(const mykfa_bwd_params* p, void* workspace, size_t workspace_bytes, mykfa_stream_t stream);
+/* The two halves of mykfa_bwd_ws over every KV head in one launch each (workspace of
+ * num_kv_heads * mykfa_bwd_workspace_per_kv_head bytes, else MYKFA_ERR_WORKSPACE):
+ * dK/dV storing dS (replaces _bwd_dkdv_kernel, flash_attn.py:264-314; reads delta, so run
+ * mykfa_bwd_preprocess first), then dQ from the stored dS (replaces _bwd_dq_kernel,
+ * flash_attn.py:181-230, without its S / dP recompute). */
+int mykfa_bwd_dkdv_ws(const mykfa_bwd_params* p, void* workspace, size_t workspace_bytes, mykfa_stream_t stream);
+int mykfa_bwd_dq_ws(const mykfa_bwd_params* p, void* workspace, size_t workspace_bytes, mykfa_stream_t stream);
 
 /* ---- KV-cache decode (split-K) ------------------------------------------------------ */
 /* Split count the library would pick for this shape (>= 1): about 88 keys per split per query

@@ -12,7 +12,7 @@ import os
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmykfa.so"
-ABI_VERSION = 6  # MYKFA_ABI_VERSION
+ABI_VERSION = 7  # MYKFA_ABI_VERSION
 
 OK = 0
 ERR_INVALID = 1
@@ -150,6 +150,10 @@ SIGNATURES = {
     "mykfa_bwd_dkdv": (ctypes.c_int, [ctypes.POINTER(BwdParams), _ptr]),
     "mykfa_bwd_dq": (ctypes.c_int, [ctypes.POINTER(BwdParams), _ptr]),
     "mykfa_bwd": (ctypes.c_int, [ctypes.POINTER(BwdParams), _ptr]),
+    "mykfa_bwd_workspace_per_kv_head": (ctypes.c_size_t, [ctypes.POINTER(BwdParams)]),
+    "mykfa_bwd_ws": (ctypes.c_int, [ctypes.POINTER(BwdParams), _ptr, ctypes.c_size_t, _ptr]),
+    "mykfa_bwd_dkdv_ws": (ctypes.c_int, [ctypes.POINTER(BwdParams), _ptr, ctypes.c_size_t, _ptr]),
+    "mykfa_bwd_dq_ws": (ctypes.c_int, [ctypes.POINTER(BwdParams), _ptr, ctypes.c_size_t, _ptr]),
     "mykfa_decode_num_splits": (ctypes.c_int, [_i32, _i32, _i32, _i32, _i32]),
     "mykfa_decode_workspace_size": (ctypes.c_size_t, [_i32, _i32, _i32, _i32, _i32]),
     "mykfa_decode_splitk": (ctypes.c_int, [ctypes.POINTER(DecodeParams), _ptr, ctypes.c_size_t, _ptr]),

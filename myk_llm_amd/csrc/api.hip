@@ -373,6 +373,46 @@ int mykfa_bwd(const mykfa_bwd_params* p, mykfa_stream_t stream) {
     return mykfa_bwd_dkdv(p, stream);
 }
 
+size_t mykfa_bwd_workspace_per_kv_head(const mykfa_bwd_params* p) {
+    if (check_bwd(p)) return 0;
+    return mykfa::bwd_ds_bytes_per_kv_head(*p);
+}
+
+int mykfa_bwd_ws(const mykfa_bwd_params* p, void* workspace, size_t workspace_bytes, mykfa_stream_t stream) {
+    int rc = check_bwd(p);
+    if (rc) return rc;
+    const size_t per = mykfa::bwd_ds_bytes_per_kv_head(*p);
+    if (per == 0 || workspace_bytes < per) return mykfa_bwd(p, stream);
+    if (workspace == nullptr) return fail(MYKFA_ERR_INVALID, "workspace is NULL");
+    const size_t heads = workspace_bytes / per;
+    const int per_pass = heads < (size_t)p->fwd.num_kv_heads ? (int)heads : p->fwd.num_kv_heads;
+    return launched(mykfa::launch_bwd_ds(*p, workspace, per_pass, as_stream(stream)), "mykfa_bwd_ws");
+}
+
+namespace {
+int bwd_ds_half(const mykfa_bwd_params* p, void* workspace, size_t workspace_bytes, mykfa_stream_t stream,
+                bool dq, const char* what) {
+    int rc = check_bwd(p);
+    if (rc) return rc;
+    const size_t per = mykfa::bwd_ds_bytes_per_kv_head(*p);
+    if (per == 0) return fail(MYKFA_ERR_UNSUPPORTED, "%s: no stored-dS path for head_dim %d", what, p->fwd.head_dim);
+    const size_t need = per * (size_t)p->fwd.num_kv_heads;
+    if (workspace_bytes < need)
+        return fail(MYKFA_ERR_WORKSPACE, "%s: workspace of %zu bytes, %zu needed (every KV head's dS)", what,
+                    workspace_bytes, need);
+    if (workspace == nullptr) return fail(MYKFA_ERR_INVALID, "workspace is NULL");
+    return launched(mykfa::launch_bwd_ds_half(*p, workspace, dq, as_stream(stream)), what);
+}
+}  // namespace
+
+int mykfa_bwd_dkdv_ws(const mykfa_bwd_params* p, void* workspace, size_t workspace_bytes, mykfa_stream_t stream) {
+    return bwd_ds_half(p, workspace, workspace_bytes, stream, false, "mykfa_bwd_dkdv_ws");
+}
+
+int mykfa_bwd_dq_ws(const mykfa_bwd_params* p, void* workspace, size_t workspace_bytes, mykfa_stream_t stream) {
+    return bwd_ds_half(p, workspace, workspace_bytes, stream, true, "mykfa_bwd_dq_ws");
+}
+
 int mykfa_decode_num_splits(int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t seqlen_q,
                             int32_t capacity) {
     return mykfa::decode_default_splits(batch, num_heads, num_kv_heads, seqlen_q, capacity);

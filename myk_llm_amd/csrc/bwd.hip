@@ -1,5 +1,7 @@
-// Backward pass (replaces _bwd_dq_kernel and _bwd_dkdv_kernel, flash_attn.py:157-314).
-// Two launches in stream order, no atomics (results are bitwise deterministic):
+// Backward pass (replaces _bwd_dq_kernel and _bwd_dkdv_kernel, flash_attn.py:157-314). No
+// atomics anywhere: results are bitwise deterministic. Two schedules over the same kernels:
+//
+// Recomputing (mykfa_bwd; every head_dim): two launches in stream order.
 //   1. dQ: forward-shaped: delta = rowsum(dO * O) for the workgroup's rows first (the
 //      preprocess fused into _bwd_dq_kernel, flash_attn.py:215-216), written for pass 2; then
 //      S^T = K Q^T, dP^T = V dO^T, dS^T = P^T (dP^T - delta), and dQ^T += K^T dS^T with K^T read
@@ -11,10 +13,16 @@
 //      dP = dO V^T (A operands: row reads of the LDS Q/dO tiles), P = exp2(S * c - lse),
 //      dS = P (dP - delta), then dV^T += dO^T P and dK^T += Q^T dS with dO^T / Q^T taken by the
 //      LDS transpose read.
-// bwd_preprocess_kernel computes delta alone (mykfa_bwd_preprocess), for callers that run
-// dK/dV without dQ. All products are 32x32x16 bf16 (or fp16) MFMA with fp32 accumulation;
-// P and dS are rounded to the input type before their products, as in flash_attn.py:177,
-// :257, :260.
+//
+// Stored dS (mykfa_bwd_ws; head_dim 128): delta by bwd_delta_kernel, then per pass of KV heads
+// the dK/dV kernel above, which also stores each 32 x 32 block of dS (bf16, the value its dK
+// product uses) into a caller's workspace, and bwd_dq_ds_kernel, which forms dQ = dS K from
+// those blocks: five products per (query tile, key block) pair instead of seven, paid for
+// with one write and one read of dS through HBM.
+//
+// bwd_delta_kernel alone is mykfa_bwd_preprocess, for callers that run dK/dV without dQ. All
+// products are 32x32x16 bf16 (or fp16) MFMA with fp32 accumulation; P and dS are rounded to
+// the input type before their products, as in flash_attn.py:177, :257, :260.
 #include "common.h"
 #include "kernels.h"
 
@@ -47,31 +55,71 @@ struct BwdArgs {
     int num_heads;
     int batch;
     int gx, gy, gz;  // blocks per (group, sequence), sequences, groups; decoded by block_coord
+    // Stored dS (the dK/dV pass writes it, the dS-driven dQ pass reads it). A pass covers the
+    // query heads of KV heads kv0, kv0 + 1, ...; its r-th query head's blocks start at
+    // ds + r * ds_hs; there, query tile t (ds_tile_base + tile within its sequence, < ds_nqt)
+    // owns a row of ds_w 32 x 32 blocks, at slot = key block - the first key block it sees.
+    uint16_t* ds;
+    int64_t ds_hs;
+    int ds_w, ds_nqt;
+    int kv0;
 };
+
+typedef __attribute__((address_space(1))) s16x8 gs16x8;
+
+// First 32-key block a 32-row query tile i sees (the tile's band starts at key 32 i + lo_f).
+__device__ inline int ds_first_block(int i, int lo_f) { return max(i + (lo_f >> 5), 0); }
+// Index of a sequence's first query tile in the dS rows: packed sequences start at
+// floor(tok0 / 32) + b, which keeps every sequence's tiles apart; dense batches at b * tiles.
+__device__ inline int ds_tile_base(int b, int64_t tok0, int seqlen_q, bool varlen) {
+    return varlen ? (int)(tok0 >> 5) + b : b * ((seqlen_q + 31) >> 5);
+}
 
 // ---- 1. delta = rowsum(dO * O) ---------------------------------------------------------
 
+// One flat grid over the (row, head) items: rows run over the packed tokens (varlen:
+// cu_seqlens_q[0] .. cu_seqlens_q[batch]) or batch x seqlen_q (dense), heads fastest, D / 8
+// lanes per item; each lane keeps U items' loads in flight and the grid strides over the
+// rest (a per-sequence grid sized by max_seqlen left most workgroups idle on packed batches:
+// 41 -> 28 us at 16384 packed tokens, 16 heads, D = 128).
 template <int D, typename T>
-__global__ __launch_bounds__(256) void bwd_preprocess_kernel(BwdArgs a) {
-    constexpr int CPR = D / 8;         // lanes per (token, head) row
-    constexpr int RPB = 256 / CPR;     // rows per block
-    const int b = blockIdx.y;
-    SeqInfo qs = seq_info(b, a.cu_q, nullptr, a.seqlen_q, false);
-    const int64_t item = (int64_t)blockIdx.x * RPB + threadIdx.x / CPR;  // over (token, head)
+__global__ __launch_bounds__(256) void bwd_delta_kernel(BwdArgs a) {
+    constexpr int CPR = D / 8;
+    constexpr int IPB = 256 / CPR;  // items per block per pass
+    constexpr int U = 4;
+    const bool varlen = a.cu_q != nullptr;
+    const int r_lo = varlen ? a.cu_q[0] : 0;
+    const int r_hi = varlen ? a.cu_q[a.batch] : a.batch * a.seqlen_q;
+    const int64_t n = (int64_t)(r_hi - r_lo) * a.num_heads;
     const int ch = threadIdx.x % CPR;
-    const int tok = item / a.num_heads, h = item % a.num_heads;
-    float s = 0.f;
-    const bool ok_row = tok < qs.len;
-    if (ok_row) {
-        const uint16_t* op = a.o + (int64_t)b * a.obs + (qs.tok0 + tok) * a.ots + (int64_t)h * a.ohs + ch * 8;
-        const uint16_t* dp = a.dout + (int64_t)b * a.dobs + (qs.tok0 + tok) * a.dots + (int64_t)h * a.dohs + ch * 8;
-        s16x8 ov = ld16(op), dv = ld16(dp);
+    const int64_t stride = (int64_t)gridDim.x * IPB;
+    for (int64_t base = (int64_t)blockIdx.x * IPB + threadIdx.x / CPR; base < n; base += stride * U) {
+        s16x8 ov[U], dv[U];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) s += T::to_float((uint16_t)ov[i]) * T::to_float((uint16_t)dv[i]);
+        for (int u = 0; u < U; ++u) {
+            const int64_t item = base + u * stride;
+            ov[u] = dv[u] = s16x8{0, 0, 0, 0, 0, 0, 0, 0};
+            if (item < n) {
+                const int r = r_lo + (int)(item / a.num_heads), h = (int)(item % a.num_heads);
+                const int bi = varlen ? 0 : r / a.seqlen_q, t = varlen ? r : r % a.seqlen_q;
+                ov[u] = ld16(a.o + (int64_t)bi * a.obs + (int64_t)t * a.ots + (int64_t)h * a.ohs + ch * 8);
+                dv[u] = ld16(a.dout + (int64_t)bi * a.dobs + (int64_t)t * a.dots + (int64_t)h * a.dohs + ch * 8);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            float sum = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) sum += T::to_float((uint16_t)ov[u][i]) * T::to_float((uint16_t)dv[u][i]);
+#pragma unroll
+            for (int off = 1; off < CPR; off <<= 1) sum += __shfl_xor(sum, off);
+            const int64_t item = base + u * stride;
+            if (item < n && ch == 0) {
+                const int r = r_lo + (int)(item / a.num_heads), h = (int)(item % a.num_heads);
+                a.delta[(int64_t)h * a.lse_hs + r] = sum;
+            }
+        }
     }
-#pragma unroll
-    for (int off = 1; off < CPR; off <<= 1) s += __shfl_xor(s, off);
-    if (ok_row && ch == 0) a.delta[(int64_t)h * a.lse_hs + qs.row0 + tok] = s;
 }
 
 // ---- 2. dK / dV -------------------------------------------------------------------------
@@ -103,8 +151,9 @@ __device__ inline s16x8 lds_tr_op(const uint16_t* tile, int db, int kb, int lane
 // keys' K and V in registers as B operands and streams its own (Q, dO, lse, delta) query
 // tiles through a wave-private asynchronous LDS ring: the main loop has no workgroup
 // barrier. The hpw partial dK/dV of a key block are summed through LDS in a fixed order
-// (deterministic) at the end.
-template <int D, int NW, int STAGES, typename T>
+// (deterministic) at the end. With DS, every 32 x 32 dS block is also stored (bf16, the
+// rounding its dV/dK product uses) for the dS-driven dQ pass: key-major, 32 queries per key.
+template <int D, int NW, int STAGES, typename T, bool DS>
 __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
     constexpr int KD = D / 16;
     constexpr int DB = (D + 31) / 32;
@@ -127,7 +176,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
     // every sequence and rank 0 (the first key block of the longest sequences) starts first.
     const BlockCoord bc = block_coord(xcd_logical(blockIdx.x), a.gz, a.gy, a.cu_k != nullptr);
     if (bc.rank >= a.gx) return;
-    const int kvh = bc.group;
+    const int kvh = a.kv0 + bc.group;
     const int b = bc.seq;
     SeqInfo ks = seq_info(b, a.cu_k, nullptr, a.seqlen_k, false);
     const int k_len = ks.len;
@@ -286,13 +335,48 @@ __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
         if (t < iters) issue();
     if constexpr (D <= 128) load_kv();
 
+    // dS: byte address of the current head's (pass-relative) first tile row of this sequence,
+    // moved on by hpw heads per head change; the lane's 16-byte chunk within a block.
+    uint64_t ds_ptr = 0, ds_hstep = 0;
+    int ds_w = 0, ds_rows = 0, ds_jblk = 0, ds_lob = 0;
+    if constexpr (DS) {
+        const int t0 = ds_tile_base(b, qs.tok0, a.seqlen_q, a.cu_q != nullptr);
+        ds_w = sgpr_copy(a.ds_w);
+        ds_rows = sgpr_copy(a.ds_nqt) - t0;
+        ds_hstep = (uint64_t)hpw * (uint64_t)a.ds_hs * 2;
+        ds_ptr = reinterpret_cast<uint64_t>(a.ds) +
+                 ((uint64_t)((int64_t)(kvh - a.kv0) * a.group + hs) * (uint64_t)a.ds_hs + (uint64_t)t0 * ds_w * 1024) * 2;
+        ds_jblk = nw0 >> 5;
+        ds_lob = lo_f >> 5;
+    }
+    const unsigned ds_lane = (unsigned)(l32 * 64 + 16 * g);
+    const bool partial_block = bs < 32;
+    // A tile's dS block is stored at the top of the NEXT iteration, right after its ring wait:
+    // stores share the vector memory counter with the ring loads, and a store issued before
+    // a refill would hold up the wait for the tile after it until the store completed.
+    s16x8 ds_keep[2] = {s16x8{0, 0, 0, 0, 0, 0, 0, 0}, s16x8{0, 0, 0, 0, 0, 0, 0, 0}};
+    uint64_t ds_keep_at = 0;
+    bool ds_keep_ok = false;
+    auto ds_flush = [&]() {
+        if (ds_keep_ok) {
+            // Global (not generic) address space: a flat store would also count against the
+            // LDS counter and hold up every LDS wait until it completed.
+            gs16x8* dsp = reinterpret_cast<gs16x8*>(ds_keep_at + ds_lane);
+            dsp[0] = ds_keep[0];
+            dsp[2] = ds_keep[1];
+        }
+        ds_keep_ok = false;
+    };
+
     int cur_tile = 0, cur_stage = 0;
     for (int it = 0; it < iters; ++it) {
         const int after = iters - 1 - it < STAGES - 1 ? iters - 1 - it : STAGES - 1;
         ring_wait<LOADS, STAGES + 1>(after);  // tile it landed; up to STAGES - 1 later tiles in flight
+        if constexpr (DS) ds_flush();
         const int m0 = wr.lo + cur_tile * BMQ;
         const bool masked = !(m0 >= wr.mid_lo && m0 + BMQ <= wr.mid_hi);
         const uint16_t* st = ring + cur_stage * STAGE;
+        const bool head_done = cur_tile + 1 == ntiles;
         cur_tile = cur_tile + 1 == ntiles ? 0 : cur_tile + 1;
         cur_stage = cur_stage + 1 == STAGES ? 0 : cur_stage + 1;
         const uint16_t* Qs = st;
@@ -358,6 +442,19 @@ __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
             pb[kb] = __builtin_bit_cast(s16x8, pw);
             dsb[kb] = __builtin_bit_cast(s16x8, dw);
         }
+        if constexpr (DS) {
+            // Block (tile m0 / 32, key block nw0 / 32): lane (key l32, g) holds queries
+            // 16 kb + 8 g + 0..7 of its key. Keys past the sequence are stored as 0 (their K
+            // rows are 0 and their scores unmasked inside the band's full tiles).
+            const int ti = m0 >> 5;
+            const int slot = ds_jblk - max(ti + ds_lob, 0);  // ds_first_block(ti, lo_f)
+            ds_keep[0] = dsb[0];
+            ds_keep[1] = dsb[1];
+            if (partial_block && key >= k_len) ds_keep[0] = ds_keep[1] = s16x8{0, 0, 0, 0, 0, 0, 0, 0};
+            ds_keep_ok = slot < ds_w && ti < ds_rows;
+            ds_keep_at = ds_ptr + (uint64_t)(ti * ds_w + slot) * 2048;
+            if (head_done) ds_ptr += ds_hstep;
+        }
         // With the transposed operands already in registers the stage is free: refill it now
         // (this wave's reads of it have returned), ahead of the dV/dK products.
         if constexpr (PF) {
@@ -382,6 +479,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
             if (it + STAGES < iters) issue();
         }
     }
+    if constexpr (DS) ds_flush();
 
     // Sum the hpw partials of each key block in a fixed order (waves hs = 1.. into hs = 0).
     if (hpw > 1) {
@@ -624,6 +722,176 @@ __global__ __launch_bounds__(NW * 64) void bwd_dq_kernel(BwdArgs a) {
     }
 }
 
+// ---- 4. dQ from the stored dS ------------------------------------------------------------
+
+// B operand (16 keys x 32 queries) of a 32 x 32 dS block stored key-major in LDS (32 queries
+// per 64-byte row, unswizzled): lane holds blk[16 kb + 8 g + i][l32], i = 0..7, by two
+// transpose reads (4 rows x 16 columns per 16-lane group each).
+__device__ inline s16x8 lds_tr_block32(const uint16_t* blk, int kb, int lane) {
+    const int G = lane >> 4, jj = lane & 15;
+    const int col = 16 * (G & 1) + 4 * (jj & 3);
+    const int row = 16 * kb + 8 * (G >> 1) + (jj >> 2);
+    return cat4(ds_read_tr(blk + row * 32 + col), ds_read_tr(blk + (row + 4) * 32 + col));
+}
+
+// dQ = sm_scale * dS K over the band from the dS blocks the dK/dV pass stored: one product per
+// (query tile, key block) pair where the recomputing kernel above takes three (S and dP
+// again). Workgroup = NW waves: hpw query heads of one GQA group x NW / hpw blocks of 64 query
+// rows (two 32-row tiles per wave). Per step of NBK 32-key blocks a STAGES-deep direct-to-LDS
+// ring brings the K rows (shared by the workgroup's heads) and each wave's 2 x NBK dS blocks
+// (a block outside its tile's band is fetched through an empty buffer range, i.e. as zeros,
+// so every wave issues the same loads per step). dQ^T += K^T dS^T with both operands read
+// transposed. The pass streams each stored byte once: HBM-bound, except along the longest
+// causal rows, whose chain of steps is covered by the ring's depth.
+template <int D, int NW, int NBK, int STAGES, typename T>
+__global__ __launch_bounds__(NW * 64) void bwd_dq_ds_kernel(BwdArgs a) {
+    constexpr int DB = D / 32;
+    constexpr int RQ = 64;
+    constexpr int BN = 32 * NBK;
+    using KRing = TileRing<D, BN, 1, NW>;
+    constexpr int LOADS = KRing::LOADS + 4 * NBK;  // K share + 2 x NBK dS blocks of 2 KB
+    constexpr int KT = BN * D;
+    constexpr int DSW = 2 * NBK * 1024;            // one wave's dS blocks per stage
+    constexpr int STAGE = KT + NW * DSW;
+    static_assert(D % 32 == 0, "whole 32-column blocks");
+    __shared__ __attribute__((aligned(16))) uint16_t smem[STAGES][STAGE];
+
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int l32 = lane & 31, g = lane >> 5;
+    const int hpw = a.hpw, kpw = NW / hpw;
+    // Longest causal rows first across all heads and sequences, XCD-grouped.
+    const BlockCoord bc = block_coord(xcd_logical(blockIdx.x), a.gz, a.gy, a.cu_q != nullptr);
+    if (bc.rank >= a.gx) return;
+    const int b = bc.seq;
+    SeqInfo qs = seq_info(b, a.cu_q, nullptr, a.seqlen_q, false);
+    const int tok_base = (a.gx - 1 - bc.rank) * kpw * RQ;
+    if (tok_base >= qs.len) return;
+    SeqInfo ks = seq_info(b, a.cu_k, nullptr, a.seqlen_k, false);
+    const int q_len = qs.len, k_len = ks.len;
+    const int hrel = bc.group * hpw + wave % hpw;  // query head within the pass
+    const int h = a.kv0 * a.group + hrel;
+    const int kvh = a.kv0 + bc.group * hpw / a.group;
+    const int lo_f = band_lo(k_len, q_len, a.wl), hi_f = band_hi(k_len, q_len, a.wr);
+
+    // Key range of the workgroup (union of its tiles' ranges) and this wave's two tiles.
+    int wg_lo = 1 << 30, wg_hi = 0;
+    for (int tt = 0; tt < 2 * kpw; ++tt) {
+        const int s0 = tok_base + 32 * tt;
+        const int bs = q_len - s0 < 32 ? q_len - s0 : 32;
+        if (bs <= 0) break;
+        const Ranges r = block_ranges(s0, bs, lo_f, hi_f, k_len, 32);
+        if (r.hi > r.lo) {
+            wg_lo = r.lo < wg_lo ? r.lo : wg_lo;
+            wg_hi = r.hi > wg_hi ? r.hi : wg_hi;
+        }
+    }
+    const int nsteps = wg_hi > wg_lo ? (wg_hi - wg_lo + BN - 1) / BN : 0;
+    const int s_w = tok_base + (wave / hpw) * RQ;
+    const int ds_t0 = ds_tile_base(b, qs.tok0, a.seqlen_q, a.cu_q != nullptr);
+    int blo[2], bhi[2];
+    uint64_t ds_row[2];  // byte address of each tile's slot 0 minus its first block
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+        const int s0 = s_w + 32 * tt;
+        const int bs = q_len - s0 < 32 ? q_len - s0 : 32;
+        blo[tt] = bhi[tt] = 0;
+        const int row = ds_t0 + (s0 >> 5);
+        if (bs > 0 && row < a.ds_nqt) {
+            const Ranges r = block_ranges(s0, bs, lo_f, hi_f, k_len, 32);
+            if (r.hi > r.lo) {
+                blo[tt] = ds_first_block(s0 >> 5, lo_f);  // = r.lo / 32
+                bhi[tt] = (r.hi + 31) >> 5;
+                bhi[tt] = bhi[tt] - blo[tt] > a.ds_w ? blo[tt] + a.ds_w : bhi[tt];
+            }
+        }
+        ds_row[tt] = reinterpret_cast<uint64_t>(a.ds) +
+                     (uint64_t)(((int64_t)hrel * a.ds_hs + ((int64_t)row * a.ds_w - blo[tt]) * 1024) * 2);
+    }
+
+    const uint16_t* kbase = a.k + (int64_t)b * a.kbs + ks.tok0 * a.kts + (int64_t)kvh * a.khs;
+    const i32x4 rsrc[1] = {rows_rsrc(kbase, k_len, a.kts, D)};
+    const int tstride[1] = {(int)(a.kts * 2)};
+    const int j0 = wg_lo >> 5;
+    auto issue = [&](int t) {
+        uint16_t* st = smem[t % STAGES];
+        uint16_t* tiles[1] = {st};
+        KRing::issue(rsrc, tstride, tiles, wg_lo + BN * t, wave, lane);
+#pragma unroll
+        for (int kb = 0; kb < NBK; ++kb) {
+            const int j = j0 + NBK * t + kb;
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                const bool vis = j >= blo[tt] && j < bhi[tt];
+                const i32x4 r = buffer_rsrc32(ds_row[tt] + (uint64_t)j * 2048, vis ? 2048 : 0);
+                const uint32_t dst = lds_addr(st + KT + wave * DSW + (kb * 2 + tt) * 1024);
+                dma16_nt(r, dst, lane * 16);
+                dma16_nt(r, dst + 1024, 1024 + lane * 16);
+            }
+        }
+    };
+
+    f32x16 acc[2][DB];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[tt][db][r] = 0.f;
+
+#pragma unroll
+    for (int t = 0; t < STAGES - 1; ++t)
+        if (t < nsteps) issue(t);
+    for (int t = 0; t < nsteps; ++t) {
+        const int after = nsteps - 1 - t < STAGES - 2 ? nsteps - 1 - t : STAGES - 2;
+        ring_wait<LOADS, STAGES>(after);
+        barrier_lds();
+        if (t + STAGES - 1 < nsteps) issue(t + STAGES - 1);
+        const uint16_t* Ks = smem[t % STAGES];
+        const uint16_t* Ds = Ks + KT + wave * DSW;
+#pragma unroll
+        for (int kb = 0; kb < NBK; ++kb) {
+            const int j = j0 + NBK * t + kb;
+            const bool v0 = j >= blo[0] && j < bhi[0], v1 = j >= blo[1] && j < bhi[1];
+            if (!(v0 || v1)) continue;
+            s16x8 kt[DB][2];
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk) kt[db][kk] = lds_tr_op<D>(Ks, db, 2 * kb + kk, lane);
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                if (!(tt == 0 ? v0 : v1)) continue;
+                const uint16_t* blk = Ds + (kb * 2 + tt) * 1024;
+                const s16x8 d0 = lds_tr_block32(blk, 0, lane);
+                const s16x8 d1 = lds_tr_block32(blk, 1, lane);
+#pragma unroll
+                for (int db = 0; db < DB; ++db) {
+                    acc[tt][db] = T::mfma32(kt[db][0], d0, acc[tt][db]);
+                    acc[tt][db] = T::mfma32(kt[db][1], d1, acc[tt][db]);
+                }
+            }
+        }
+    }
+
+    // dQ^T rows = d (registers), columns = queries (lanes): 8-byte stores of 4 consecutive d.
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+        const int qi = s_w + 32 * tt + l32;
+        if (qi >= q_len) continue;
+        uint16_t* dqp = a.dq + (int64_t)b * a.dqbs + (qs.tok0 + qi) * a.dqts + (int64_t)h * a.dqhs;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int rq = 0; rq < 4; ++rq) {
+                const int d0 = 32 * db + 8 * rq + 4 * g;
+                const f32x16& c = acc[tt][db];
+                u32x2 w = {T::pack2(c[4 * rq] * a.sm_scale, c[4 * rq + 1] * a.sm_scale),
+                           T::pack2(c[4 * rq + 2] * a.sm_scale, c[4 * rq + 3] * a.sm_scale)};
+                *reinterpret_cast<u32x2*>(dqp + d0) = w;
+            }
+    }
+}
+
 int gcd_int(int x, int y) {
     while (y) {
         int t = x % y;
@@ -667,26 +935,35 @@ BwdArgs make_args(const mykfa_bwd_params& p) {
     a.hpw = 1;  // set per kernel shape by its launcher
     a.num_heads = f.num_heads;
     a.batch = f.batch;
+    a.ds = nullptr;
+    a.ds_hs = 0;
+    a.ds_w = a.ds_nqt = 0;
+    a.kv0 = 0;
     return a;
 }
 
 template <typename T>
 hipError_t preprocess_dtype(const BwdArgs& a, int D, hipStream_t s) {
-    const int rpb = 256 / (D / 8);
-    const long long items = (long long)a.seqlen_q * a.num_heads;
-    dim3 grid((unsigned)((items + rpb - 1) / rpb), a.batch);
+    // Items = rows x heads over at most the rows the launch covers (the varlen row count is
+    // read on the device); enough blocks for every lane to keep U items in flight once.
+    const long long rows = (long long)a.batch * a.seqlen_q;
+    const long long items = rows * a.num_heads;
+    const long long per_block = (256 / (D / 8)) * 4;
+    long long blocks = (items + per_block - 1) / per_block;
+    blocks = blocks < 1 ? 1 : (blocks > 8192 ? 8192 : blocks);
+    dim3 grid((unsigned)blocks);
     switch (D) {
-        case 16: hipLaunchKernelGGL((bwd_preprocess_kernel<16, T>), grid, dim3(256), 0, s, a); break;
-        case 32: hipLaunchKernelGGL((bwd_preprocess_kernel<32, T>), grid, dim3(256), 0, s, a); break;
-        case 64: hipLaunchKernelGGL((bwd_preprocess_kernel<64, T>), grid, dim3(256), 0, s, a); break;
-        case 128: hipLaunchKernelGGL((bwd_preprocess_kernel<128, T>), grid, dim3(256), 0, s, a); break;
-        case 256: hipLaunchKernelGGL((bwd_preprocess_kernel<256, T>), grid, dim3(256), 0, s, a); break;
+        case 16: hipLaunchKernelGGL((bwd_delta_kernel<16, T>), grid, dim3(256), 0, s, a); break;
+        case 32: hipLaunchKernelGGL((bwd_delta_kernel<32, T>), grid, dim3(256), 0, s, a); break;
+        case 64: hipLaunchKernelGGL((bwd_delta_kernel<64, T>), grid, dim3(256), 0, s, a); break;
+        case 128: hipLaunchKernelGGL((bwd_delta_kernel<128, T>), grid, dim3(256), 0, s, a); break;
+        case 256: hipLaunchKernelGGL((bwd_delta_kernel<256, T>), grid, dim3(256), 0, s, a); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
 
-template <int D, int NW, int STAGES, typename T>
+template <int D, int NW, int STAGES, typename T, bool DS = false>
 hipError_t dkdv_launch(BwdArgs a, int num_kv_heads, hipStream_t s) {
     a.hpw = gcd_int(a.group, NW);
     const int keys_per_wg = 32 * (NW / a.hpw);
@@ -696,7 +973,7 @@ hipError_t dkdv_launch(BwdArgs a, int num_kv_heads, hipStream_t s) {
     const long long n = block_grid_size(a.gx, a.gz, a.gy, a.cu_k != nullptr);
     if (n == 0) return hipSuccess;
     if (n > (1LL << 30)) return hipErrorInvalidConfiguration;
-    hipLaunchKernelGGL((bwd_dkdv_kernel<D, NW, STAGES, T>), dim3(xcd_grid((int)n)), dim3(NW * 64), 0, s, a);
+    hipLaunchKernelGGL((bwd_dkdv_kernel<D, NW, STAGES, T, DS>), dim3(xcd_grid((int)n)), dim3(NW * 64), 0, s, a);
     return hipGetLastError();
 }
 
@@ -738,7 +1015,83 @@ hipError_t dq_dtype(const BwdArgs& a, int D, hipStream_t s) {
     }
 }
 
+// dS-driven dQ over the pass's num_kv_heads KV heads (a.kv0 on).
+template <int D, int NW, int NBK, int STAGES, typename T>
+hipError_t dq_ds_launch(BwdArgs a, int num_kv_heads, hipStream_t s) {
+    a.hpw = gcd_int(a.group, NW);
+    const int rows_per_wg = 64 * (NW / a.hpw);
+    a.gx = (a.seqlen_q + rows_per_wg - 1) / rows_per_wg;
+    a.gy = a.batch;
+    a.gz = num_kv_heads * a.group / a.hpw;
+    const long long n = block_grid_size(a.gx, a.gz, a.gy, a.cu_q != nullptr);
+    if (n == 0) return hipSuccess;
+    if (n > (1LL << 30)) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL((bwd_dq_ds_kernel<D, NW, NBK, STAGES, T>), dim3(xcd_grid((int)n)), dim3(NW * 64), 0, s, a);
+    return hipGetLastError();
+}
+
+// Delta, then per pass of kv_per_pass KV heads: dK/dV storing dS, and dQ from dS.
+template <typename T>
+hipError_t ds_passes(BwdArgs a, const mykfa_bwd_params& p, int kv_per_pass, hipStream_t s) {
+    hipError_t e = preprocess_dtype<T>(a, p.fwd.head_dim, s);
+    for (int kv0 = 0; e == hipSuccess && kv0 < p.fwd.num_kv_heads; kv0 += kv_per_pass) {
+        const int n = p.fwd.num_kv_heads - kv0 < kv_per_pass ? p.fwd.num_kv_heads - kv0 : kv_per_pass;
+        a.kv0 = kv0;
+        // dQ: 64 keys per step, 3 stages (144 KB of LDS: one workgroup per CU) measured best
+        // among 32 / 64 keys per step and 2-6 stages (the single-workgroup ring holds the most
+        // bytes in flight).
+        e = dkdv_launch<128, 4, 2, T, true>(a, n, s);
+        if (e == hipSuccess) e = dq_ds_launch<128, 4, 2, 3, T>(a, n, s);
+    }
+    return e;
+}
+
+// Rows of the dS layout: query tiles over the whole launch (see ds_tile_base) and the slots per
+// tile (the most 32-key blocks one 32-row tile's band can touch).
+int64_t ds_tiles(const mykfa_fwd_params& f) {
+    if (f.cu_seqlens_q != nullptr) return f.lse_head_stride / 32 + f.batch + 1;
+    return (int64_t)f.batch * ((f.max_seqlen_q + 31) / 32);
+}
+int64_t ds_slots(const mykfa_fwd_params& f) {
+    const int64_t all = (f.max_seqlen_k + 31) / 32;
+    const int64_t band = (32 + (int64_t)f.window_left + f.window_right + 31) / 32 + 1;
+    return all < band ? all : band;
+}
+
 }  // namespace
+
+size_t bwd_ds_bytes_per_kv_head(const mykfa_bwd_params& p) {
+    const mykfa_fwd_params& f = p.fwd;
+    // Only head_dim 128: at 64 the dK/dV pass's stores and the separate delta pass cost more
+    // than the recomputed S and dP they save (measured on packed and dense batches).
+    if (f.head_dim != 128) return 0;
+    if (f.batch <= 0 || f.max_seqlen_q <= 0 || f.max_seqlen_k <= 0) return 0;
+    const int64_t group = f.num_heads / f.num_kv_heads;
+    return (size_t)(group * ds_tiles(f) * ds_slots(f)) * 2048;
+}
+
+BwdArgs ds_args(const mykfa_bwd_params& p, void* ws) {
+    BwdArgs a = make_args(p);
+    a.ds = static_cast<uint16_t*>(ws);
+    a.ds_w = (int)ds_slots(p.fwd);
+    a.ds_nqt = (int)ds_tiles(p.fwd);
+    a.ds_hs = (int64_t)a.ds_nqt * a.ds_w * 1024;
+    return a;
+}
+
+hipError_t launch_bwd_ds(const mykfa_bwd_params& p, void* ws, int kv_per_pass, hipStream_t stream) {
+    const BwdArgs a = ds_args(p, ws);
+    if (p.fwd.dtype == MYKFA_BF16) return ds_passes<BF16>(a, p, kv_per_pass, stream);
+    return ds_passes<FP16>(a, p, kv_per_pass, stream);
+}
+
+hipError_t launch_bwd_ds_half(const mykfa_bwd_params& p, void* ws, bool dq, hipStream_t stream) {
+    const BwdArgs a = ds_args(p, ws);
+    const int n = p.fwd.num_kv_heads;
+    if (p.fwd.dtype == MYKFA_BF16)
+        return dq ? dq_ds_launch<128, 4, 2, 3, BF16>(a, n, stream) : dkdv_launch<128, 4, 2, BF16, true>(a, n, stream);
+    return dq ? dq_ds_launch<128, 4, 2, 3, FP16>(a, n, stream) : dkdv_launch<128, 4, 2, FP16, true>(a, n, stream);
+}
 
 hipError_t launch_bwd_preprocess(const mykfa_bwd_params& p, hipStream_t stream) {
     BwdArgs a = make_args(p);

@@ -230,6 +230,14 @@ __device__ inline void dma16(i32x4 rsrc, uint32_t lds_base, uint32_t voff) {
                  : "s"(__builtin_amdgcn_readfirstlane(lds_base)), "v"(voff), "s"(rsrc)
                  : "memory", "m0");
 }
+// The same with the non-temporal hint, for data read exactly once (streamed past the caches'
+// reuse): the dS pass measured 199 -> 180 us with it.
+__device__ inline void dma16_nt(i32x4 rsrc, uint32_t lds_base, uint32_t voff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
+                 :
+                 : "s"(__builtin_amdgcn_readfirstlane(lds_base)), "v"(voff), "s"(rsrc)
+                 : "memory", "m0");
+}
 __device__ inline void dma4(i32x4 rsrc, uint32_t lds_base, uint32_t voff) {
     asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
                  :

@@ -13,6 +13,13 @@ hipError_t launch_fwd(const mykfa_fwd_params& p, hipStream_t stream);
 hipError_t launch_bwd_preprocess(const mykfa_bwd_params& p, hipStream_t stream);
 hipError_t launch_bwd_dkdv(const mykfa_bwd_params& p, hipStream_t stream);
 hipError_t launch_bwd_dq(const mykfa_bwd_params& p, hipStream_t stream);
+// Backward through stored dS: bytes of dS one KV head's query heads take (0: no such path for
+// this head_dim), and the launches (delta; per pass of kv_per_pass KV heads, dK/dV storing dS
+// into ws, then dQ from it).
+size_t bwd_ds_bytes_per_kv_head(const mykfa_bwd_params& p);
+hipError_t launch_bwd_ds(const mykfa_bwd_params& p, void* ws, int kv_per_pass, hipStream_t stream);
+// One half of it over every KV head at once: dK/dV storing dS (dq = false) or dQ from dS.
+hipError_t launch_bwd_ds_half(const mykfa_bwd_params& p, void* ws, bool dq, hipStream_t stream);
 
 // Split-K decode. The workspace holds, per (split, batch, head, query): D fp32 partial
 // outputs, then one fp32 partial lse per (split, batch, head, query).

@@ -32,6 +32,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import os
 from typing import Optional
 
 import torch
@@ -42,6 +43,14 @@ from . import _lib
 _UNBOUNDED = _lib.UNBOUNDED  # flash_attn.py:32
 _HEAD_DIMS = (16, 32, 64, 128, 256)  # flash_attn.py:322-323
 _DECODE_MAX_Q = 16  # few queries per sequence use the split-K decode kernel (flash_attn.py:364)
+
+
+def _ds_budget_bytes() -> int:
+    """Most device memory the backward may take for its stored dS (bf16, one 32 x 32 block per
+    (query tile, key block) pair of the band, bounded per query tile by the band width): 4 GiB
+    unless MYKFA_BWD_DS_MAX_MB says otherwise (0 turns the stored-dS backward off)."""
+    mb = os.environ.get("MYKFA_BWD_DS_MAX_MB")
+    return (4 << 30) if mb is None else int(mb) << 20
 
 
 # --- validation (flash_attn.py:331-350) ---------------------------------------------------
@@ -240,7 +249,15 @@ def _backward(dout: Tensor, q: Tensor, k: Tensor, v: Tensor, out: Tensor, lse: T
     p.dv_batch_stride, p.dv_token_stride, p.dv_head_stride = _strides(dv)
     L = _lib.lib()
     with _DeviceGuard(q.device):
-        _lib.check(L.mykfa_bwd(ctypes.byref(p), _stream(q.device)))
+        # dK/dV store dS and dQ is formed from it (five products per block pair instead of
+        # seven) when at least one KV head's dS fits the budget; KV heads then go in passes.
+        per_head = L.mykfa_bwd_workspace_per_kv_head(ctypes.byref(p))
+        heads = min(k.shape[-2], _ds_budget_bytes() // per_head) if per_head else 0
+        if heads > 0:
+            ws = torch.empty(heads * per_head, dtype=torch.uint8, device=q.device)
+            _lib.check(L.mykfa_bwd_ws(ctypes.byref(p), ws.data_ptr(), ws.numel(), _stream(q.device)))
+        else:
+            _lib.check(L.mykfa_bwd(ctypes.byref(p), _stream(q.device)))
     return dq, dk, dv
 
 

@@ -33,7 +33,7 @@ def test_every_declared_symbol_is_exported_and_bound(L):
 
 
 def test_version_and_struct_sizes(L):
-    assert L.mykfa_abi_version() == _lib.ABI_VERSION == 6
+    assert L.mykfa_abi_version() == _lib.ABI_VERSION == 7
     assert b"gfx950" in L.mykfa_version()
     assert L.mykfa_sizeof_fwd_params() == ctypes.sizeof(_lib.FwdParams)
     assert L.mykfa_sizeof_bwd_params() == ctypes.sizeof(_lib.BwdParams)
@@ -211,3 +211,51 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setenv("MYKFA_LIB", str(tmp_path / "nope.so"))
     with pytest.raises(RuntimeError, match="no fallback"):
         _lib.lib()
+
+
+def _bwd_params(head_dim, window_left=_lib.UNBOUNDED, window_right=0):
+    """Valid dense backward params: batch 2, 128 tokens, 8 query / 2 key-value heads."""
+    b = _lib.BwdParams()
+    f = good_fwd()
+    for t, h in (("q", 8), ("k", 2), ("v", 2), ("o", 8)):
+        setattr(f, f"{t}_batch_stride", 128 * h * head_dim)
+        setattr(f, f"{t}_token_stride", h * head_dim)
+        setattr(f, f"{t}_head_stride", head_dim)
+    f.head_dim = head_dim
+    f.window_left, f.window_right = window_left, window_right
+    b.fwd = f
+    b.dout = b.dq = b.dk = b.dv = b.delta = 0x40000
+    for pre, h in (("do", 8), ("dq", 8), ("dk", 2), ("dv", 2)):
+        setattr(b, f"{pre}_batch_stride", 128 * h * head_dim)
+        setattr(b, f"{pre}_token_stride", h * head_dim)
+        setattr(b, f"{pre}_head_stride", head_dim)
+    return b
+
+
+def test_stored_ds_workspace_size(L):
+    """mykfa_bwd_workspace_per_kv_head: one 2 KB dS block per (32-row query tile, slot) for each
+    of a KV head's query heads; slots per tile = the most 32-key blocks one tile's band can
+    touch. head_dim 128 only; 0 for other head dims and for invalid params."""
+    b = _bwd_params(128)
+    assert L.mykfa_validate_bwd(ctypes.byref(b)) == _lib.OK
+    tiles, group = 2 * 128 // 32, 4
+    # Causal, unbounded left: a tile can touch every key block of its sequence (4 of them).
+    assert L.mykfa_bwd_workspace_per_kv_head(ctypes.byref(b)) == group * tiles * 4 * 2048
+    # A 31-key left window: a tile's band spans 63 keys, i.e. at most 3 blocks.
+    b = _bwd_params(128, 31, 0)
+    assert L.mykfa_bwd_workspace_per_kv_head(ctypes.byref(b)) == group * tiles * 3 * 2048
+    assert L.mykfa_bwd_workspace_per_kv_head(ctypes.byref(_bwd_params(64))) == 0
+    b = _bwd_params(128)
+    b.dout = 0
+    assert L.mykfa_bwd_workspace_per_kv_head(ctypes.byref(b)) == 0
+
+
+def test_stored_ds_halves_check_their_workspace(L):
+    """mykfa_bwd_dkdv_ws / mykfa_bwd_dq_ws need every KV head's dS at once; both refuse a
+    smaller workspace, and head_dim 64 (no stored-dS path), before anything is launched."""
+    b = _bwd_params(128)
+    need = 2 * L.mykfa_bwd_workspace_per_kv_head(ctypes.byref(b))
+    for fn in (L.mykfa_bwd_dkdv_ws, L.mykfa_bwd_dq_ws):
+        assert fn(ctypes.byref(b), 0x50000, need - 1, None) == _lib.ERR_WORKSPACE
+        assert b"needed" in L.mykfa_last_error()
+        assert fn(ctypes.byref(_bwd_params(64)), 0x50000, 1 << 30, None) == _lib.ERR_UNSUPPORTED

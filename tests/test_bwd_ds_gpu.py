@@ -1,0 +1,219 @@
+"""The backward through stored dS (mykfa_bwd_ws, head_dim 128) on the GPU: dK/dV store every
+32 x 32 block of dS and dQ is formed from those blocks. Checked against the fp32 oracle at the
+reference's tolerance (tests/test_flash_attn.py:37-40), against the recomputing backward (mykfa_bwd: dV
+bit for bit, since P does not depend on delta; dK and dQ to bf16 rounding), and for passes
+over KV heads (a workspace of fewer heads than the launch gives the same bits) on packed and
+dense batches, windows, Lq != Lk, every GQA ratio the launchers distinguish and both dtypes."""
+
+import ctypes
+import sys
+
+import pytest
+import torch
+
+from _util import assert_close
+from myk_llm_amd import _lib
+from myk_llm_amd import flash_attn as fa
+from myk_llm_amd import flash_attn_func, flash_attn_varlen_func
+from oracle.attention import backward_reference, backward_reference_varlen
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def _problem(lens_q, lens_k, h, hk, d, dtype, dense, seed):
+    """Packed (or, with dense, (B, L, H, D)) inputs drawn on the CPU, the forward through the
+    C ABI, and a fresh dO."""
+    g = torch.Generator().manual_seed(seed)
+    if dense:
+        b, sq, sk = len(lens_q), lens_q[0], lens_k[0]
+        q = torch.randn(b, sq, h, d, generator=g).to(dtype).cuda()
+        k, v = (torch.randn(b, sk, hk, d, generator=g).to(dtype).cuda() for _ in range(2))
+        do = torch.randn(b, sq, h, d, generator=g).to(dtype).cuda()
+        cu_q = cu_k = None
+        rows = b * sq
+    else:
+        q = torch.randn(sum(lens_q), h, d, generator=g).to(dtype).cuda()
+        k, v = (torch.randn(sum(lens_k), hk, d, generator=g).to(dtype).cuda() for _ in range(2))
+        do = torch.randn(sum(lens_q), h, d, generator=g).to(dtype).cuda()
+        cu_q = torch.tensor([0] + list(torch.tensor(lens_q).cumsum(0)), dtype=torch.int32).cuda()
+        cu_k = torch.tensor([0] + list(torch.tensor(lens_k).cumsum(0)), dtype=torch.int32).cuda()
+        rows = sum(lens_q)
+    out = torch.empty_like(q)
+    lse = torch.empty((h, rows), dtype=torch.float32, device="cuda")
+    return q, k, v, do, out, lse, cu_q, cu_k
+
+
+def _params(q, k, v, out, lse, do, cu_q, cu_k, max_q, max_k, scale, wl, wr):
+    p = _lib.BwdParams()
+    p.fwd = fa._fwd_params(q, k, v, out, lse, cu_q, cu_k, None, max_q, max_k, scale, wl, wr)
+    dq, dk, dv = (torch.full_like(x, float("nan")) for x in (q, k, v))
+    delta = torch.full_like(lse, float("nan"))
+    p.dout, p.dq, p.dk, p.dv, p.delta = do.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), delta.data_ptr()
+    p.do_batch_stride, p.do_token_stride, p.do_head_stride = fa._strides(do)
+    p.dq_batch_stride, p.dq_token_stride, p.dq_head_stride = fa._strides(dq)
+    p.dk_batch_stride, p.dk_token_stride, p.dk_head_stride = fa._strides(dk)
+    p.dv_batch_stride, p.dv_token_stride, p.dv_head_stride = fa._strides(dv)
+    return p, (dq, dk, dv), delta
+
+
+CASES = [
+    # (name, lens_q, lens_k, heads, kv_heads, head_dim, window (left, right), dense)
+    ("packed causal GQA4", [300, 1, 77, 512, 33], None, 8, 2, 128, (fa._UNBOUNDED, 0), False),
+    ("packed Lq < Lk", [40, 1, 200, 64], [300, 17, 230, 64], 4, 1, 128, (fa._UNBOUNDED, 0), False),
+    ("packed Lq > Lk", [120, 70], [37, 70], 6, 2, 128, (fa._UNBOUNDED, 0), False),
+    ("dense sliding window", [700, 700], None, 4, 2, 128, (100, 0), True),
+    ("dense two-sided window", [333, 333], None, 8, 4, 128, (50, 70), True),
+    ("dense full", [257, 257, 257], None, 2, 2, 128, (fa._UNBOUNDED, fa._UNBOUNDED), True),
+    ("dense GQA8", [300], None, 8, 1, 128, (fa._UNBOUNDED, 0), True),
+    ("dense GQA3", [190, 190], None, 6, 2, 128, (fa._UNBOUNDED, 0), True),
+    ("dense GQA2 window", [260, 260], None, 4, 2, 128, (33, 0), True),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_stored_ds_backward(case, dtype):
+    name, lens_q, lens_k, h, hk, d, (wl, wr), dense = case
+    lens_k = lens_k or lens_q
+    _say(f"stored-dS backward: {name} dtype={dtype}")
+    q, k, v, do, out, lse, cu_q, cu_k = _problem(lens_q, lens_k, h, hk, d, dtype, dense, seed=5)
+    max_q, max_k = max(lens_q), max(lens_k)
+    scale = d ** -0.5
+    L = _lib.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    fp = fa._fwd_params(q, k, v, out, lse, cu_q, cu_k, None, max_q, max_k, scale, wl, wr)
+    _lib.check(L.mykfa_fwd(ctypes.byref(fp), stream))
+
+    p_ref, g_ref, _ = _params(q, k, v, out, lse, do, cu_q, cu_k, max_q, max_k, scale, wl, wr)
+    _lib.check(L.mykfa_bwd(ctypes.byref(p_ref), stream))
+    per = L.mykfa_bwd_workspace_per_kv_head(ctypes.byref(p_ref))
+    assert per > 0
+    results = []
+    for heads in (hk, 1):  # one pass over every KV head; one pass per KV head
+        p, grads, delta = _params(q, k, v, out, lse, do, cu_q, cu_k, max_q, max_k, scale, wl, wr)
+        ws = torch.full((heads * per + 100,), 0xFF, dtype=torch.uint8, device="cuda")  # NaN-filled dS
+        _lib.check(L.mykfa_bwd_ws(ctypes.byref(p), ws.data_ptr(), ws.numel(), stream))
+        results.append(grads)
+    torch.cuda.synchronize()
+    for x, y in zip(*results):
+        assert torch.equal(x, y), "passes over KV heads changed the result"
+    dq, dk, dv = results[0]
+    for x in (dq, dk, dv):
+        assert not torch.isnan(x).any(), "an unwritten dS block or gradient row was read"
+    assert torch.equal(dv, g_ref[2]), "dV differs from the recomputing backward"
+    torch.testing.assert_close(dk.float(), g_ref[1].float(), rtol=1e-2, atol=1e-2)
+    torch.testing.assert_close(dq.float(), g_ref[0].float(), rtol=2e-2, atol=2e-2)
+
+    window = (-1 if wl >= fa._UNBOUNDED else wl, -1 if wr >= fa._UNBOUNDED else wr)
+    causal = wr == 0 and window[0] == -1
+    win = (-1, -1) if causal else window
+    qc, kc, vc, doc = (x.cpu() for x in (q, k, v, do))
+    if dense:
+        exp = backward_reference(qc, kc, vc, doc, causal, win)
+    elif lens_q == lens_k:
+        exp = backward_reference_varlen(qc, kc, vc, doc, cu_q.cpu(), causal, win)
+    else:
+        exp = [torch.zeros(x.shape) for x in (qc, kc, vc)]
+        bq, bk = [0] + list(torch.tensor(lens_q).cumsum(0)), [0] + list(torch.tensor(lens_k).cumsum(0))
+        for i in range(len(lens_q)):
+            sq, sk = slice(int(bq[i]), int(bq[i + 1])), slice(int(bk[i]), int(bk[i + 1]))
+            e = backward_reference(qc[sq][None], kc[sk][None], vc[sk][None], doc[sq][None], causal, win)
+            exp[0][sq], exp[1][sk], exp[2][sk] = e[0][0], e[1][0], e[2][0]
+    for got, e in zip((dq, dk, dv), exp):
+        assert_close(got, e)
+
+
+@pytest.mark.parametrize("d", [128, 64])
+def test_without_a_head_of_workspace_it_is_the_recomputing_backward(d):
+    """With less than one KV head's dS (and at head_dim 64, which has no stored-dS path: its
+    workspace size is 0) the call is mykfa_bwd, bit for bit."""
+    _say(f"stored-dS backward: workspace below one KV head, D={d}")
+    lens = [200, 64]
+    q, k, v, do, out, lse, cu, _ = _problem(lens, lens, 8, 2, d, torch.bfloat16, False, seed=9)
+    L = _lib.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    wl, wr = fa._UNBOUNDED, 0
+    fp = fa._fwd_params(q, k, v, out, lse, cu, cu, None, 200, 200, d ** -0.5, wl, wr)
+    _lib.check(L.mykfa_fwd(ctypes.byref(fp), stream))
+    p1, g1, _ = _params(q, k, v, out, lse, do, cu, cu, 200, 200, d ** -0.5, wl, wr)
+    p2, g2, _ = _params(q, k, v, out, lse, do, cu, cu, 200, 200, d ** -0.5, wl, wr)
+    _lib.check(L.mykfa_bwd(ctypes.byref(p1), stream))
+    per = L.mykfa_bwd_workspace_per_kv_head(ctypes.byref(p2))
+    assert (per > 0) == (d == 128)
+    ws = torch.empty(max(per - 1, 16), dtype=torch.uint8, device="cuda")
+    _lib.check(L.mykfa_bwd_ws(ctypes.byref(p2), ws.data_ptr(), ws.numel(), stream))
+    torch.cuda.synchronize()
+    for x, y in zip(g1, g2):
+        assert torch.equal(x, y)
+
+
+def test_python_budget_selects_the_path(monkeypatch):
+    """The autograd backward takes the stored-dS path within MYKFA_BWD_DS_MAX_MB and the
+    recomputing one at 0; both match the oracle, and each is bitwise repeatable."""
+    _say("stored-dS backward: budget switch")
+    torch.manual_seed(3)
+    lens = [1, 17, 128, 300, 5, 64, 3]
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0)), dtype=torch.int32).cuda()
+    q = torch.randn(sum(lens), 4, 128).to(torch.bfloat16).cuda().requires_grad_()
+    k = torch.randn(sum(lens), 2, 128).to(torch.bfloat16).cuda().requires_grad_()
+    v = torch.randn(sum(lens), 2, 128).to(torch.bfloat16).cuda().requires_grad_()
+    do = torch.randn(sum(lens), 4, 128).to(torch.bfloat16).cuda()
+    grads = {}
+    for mb in ("4096", "0"):
+        monkeypatch.setenv("MYKFA_BWD_DS_MAX_MB", mb)
+        runs = []
+        for _ in range(2):
+            out = flash_attn_varlen_func(q, k, v, cu, cu, 300, 300, causal=True)
+            runs.append(torch.autograd.grad(out, (q, k, v), do))
+        for x, y in zip(*runs):
+            assert torch.equal(x, y)
+        grads[mb] = runs[0]
+    assert torch.equal(grads["4096"][2], grads["0"][2])
+    exp = backward_reference_varlen(q.detach().cpu(), k.detach().cpu(), v.detach().cpu(), do.cpu(), cu.cpu(), True,
+                                    (-1, -1))
+    for mb in grads:
+        for got, e in zip(grads[mb], exp):
+            assert_close(got, e)
+
+
+def test_dense_autograd_through_stored_ds():
+    """flash_attn_func's backward (dense, GQA, sliding window) through the default budget."""
+    _say("stored-dS backward: flash_attn_func")
+    torch.manual_seed(4)
+    q = torch.randn(2, 260, 8, 128).to(torch.bfloat16).cuda().requires_grad_()
+    k = torch.randn(2, 260, 2, 128).to(torch.bfloat16).cuda().requires_grad_()
+    v = torch.randn(2, 260, 2, 128).to(torch.bfloat16).cuda().requires_grad_()
+    do = torch.randn(2, 260, 8, 128).to(torch.bfloat16).cuda()
+    out = flash_attn_func(q, k, v, causal=True, window_size=(70, 0))
+    grads = torch.autograd.grad(out, (q, k, v), do)
+    exp = backward_reference(q.detach().cpu(), k.detach().cpu(), v.detach().cpu(), do.cpu(), True, (70, 0))
+    for got, e in zip(grads, exp):
+        assert_close(got, e)
+
+
+def test_halves_are_the_whole():
+    """mykfa_bwd_preprocess, mykfa_bwd_dkdv_ws, mykfa_bwd_dq_ws in turn give mykfa_bwd_ws's bits."""
+    _say("stored-dS backward: the two halves")
+    lens = [300, 1, 77, 512, 33]
+    q, k, v, do, out, lse, cu, _ = _problem(lens, lens, 8, 2, 128, torch.bfloat16, False, seed=6)
+    L = _lib.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    wl, wr, sc = fa._UNBOUNDED, 0, 128 ** -0.5
+    fp = fa._fwd_params(q, k, v, out, lse, cu, cu, None, 512, 512, sc, wl, wr)
+    _lib.check(L.mykfa_fwd(ctypes.byref(fp), stream))
+    p1, g1, _ = _params(q, k, v, out, lse, do, cu, cu, 512, 512, sc, wl, wr)
+    p2, g2, _ = _params(q, k, v, out, lse, do, cu, cu, 512, 512, sc, wl, wr)
+    per = L.mykfa_bwd_workspace_per_kv_head(ctypes.byref(p1))
+    ws = torch.empty(2 * per, dtype=torch.uint8, device="cuda")
+    _lib.check(L.mykfa_bwd_ws(ctypes.byref(p1), ws.data_ptr(), ws.numel(), stream))
+    _lib.check(L.mykfa_bwd_preprocess(ctypes.byref(p2), stream))
+    _lib.check(L.mykfa_bwd_dkdv_ws(ctypes.byref(p2), ws.data_ptr(), ws.numel(), stream))
+    _lib.check(L.mykfa_bwd_dq_ws(ctypes.byref(p2), ws.data_ptr(), ws.numel(), stream))
+    torch.cuda.synchronize()
+    for x, y in zip(g1, g2):
+        assert torch.equal(x, y)
