@@ -140,16 +140,30 @@ __device__ inline s16x8 cat4(s16x4 a, s16x4 b) {
 
 // ---- LDS layout -----------------------------------------------------------------------
 // Tiles of ROWS x D 16-bit elements live row-major in LDS as 16-byte chunks; chunk c of row
-// r is stored at chunk position c ^ swz(r), swz(r) = 2 (r mod 4) + bit 3 of r. The two
-// access patterns then touch 8 distinct 16-byte slots (128 bytes, every bank once):
-//  - a row-operand read (8 lanes, 16 bytes each): rows {0-3, 8-11} (or {4-7, 12-15}) of a
-//    16-row group at one chunk c (see perm32) -> swz takes the 8 values 0..7;
-//  - a transpose read (16 lanes, 8 bytes each): 4 consecutive rows r0..r0+3 at chunks c and
-//    c + 1 (c even) -> c ^ (2i + b) and (c + 1) ^ (2i + b), i = 0..3, are 8 distinct slots.
+// r is stored at chunk position c ^ swz(r). gfx950's LDS serves 64 banks x 4 bytes (256 bytes)
+// per cycle: a 16-byte-per-lane read is served 16 lanes at a time and a transpose read
+// (8 bytes per lane) 32 lanes at a time, so each such lane group must cover all 256 bytes of
+// bank space once. The two patterns of the kernels:
+//  - row-operand read: 16 lanes read rows 0..15 of an aligned 16-row group (perm32 order) at
+//    one logical chunk c;
+//  - transpose read: 32 lanes read 4 consecutive rows r0..r0+3 (r0 = 0 mod 4) at 4 aligned
+//    logical chunks 4b..4b+3 (two 8-byte halves each).
+// Per head_dim (16-byte slots of bank space: 16 per 256 bytes):
+//  - D >= 128 (a row spans >= 256 bytes): swz = 4 (r mod 4) + (r / 4 mod 4) is a bijection of
+//    the 16 rows (row read), and its top two bits, r mod 4, differ across any 4 consecutive
+//    rows, so the 4 x 4 (row, chunk) slots of a transpose read are distinct;
+//  - D = 64 (two rows per 256 bytes; slot = 8 (r mod 2) + chunk): swz = 4 (r / 2 mod 2) +
+//    (r / 4 mod 4) is a bijection on the 8 rows of each parity, and its top bit differs
+//    between rows r and r + 2;
+//  - D = 32 (four rows per 256 bytes): swz = r / 4 mod 4; D = 16 (eight rows): swz = r / 8 mod 2.
+// Measured with SQ_LDS_BANK_CONFLICT: 0 conflict cycles for both patterns (the previous
+// layout, built for 32 banks, took one conflict cycle per active cycle).
 template <int D>
 __device__ inline int lds_swz(int row) {
-    constexpr int CPR = D / 8;  // chunks per row
-    return (((row & 3) << 1) | ((row >> 3) & 1)) & (CPR - 1);
+    if constexpr (D >= 128) return ((row & 3) << 2) | ((row >> 2) & 3);
+    else if constexpr (D == 64) return (((row >> 1) & 1) << 2) | ((row >> 2) & 3);
+    else if constexpr (D == 32) return (row >> 2) & 3;
+    else return (row >> 3) & 1;
 }
 template <int D>
 __device__ inline int lds_off(int row, int col) {  // element offset of (row, col)
