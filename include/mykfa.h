@@ -341,9 +341,9 @@ int mykfa_bwd_dkdv_ws(const mykfa_bwd_params* p, void* workspace, size_t workspa
 int mykfa_bwd_dq_ws(const mykfa_bwd_params* p, void* workspace, size_t workspace_bytes, mykfa_stream_t stream);
 
 /* ---- KV-cache decode (split-K) ------------------------------------------------------ */
-/* Split count the library would pick for this shape (>= 1): about 88 keys per split per query
- * row of a KV head (352 for one query of a 4-head group), enough workgroups to fill the chip,
- * at least 128 keys per split, never a multiple of the 8 XCDs. */
+/* Split count the library would pick for this shape (>= 1): about 1400 keys per split, enough
+ * workgroups to fill the chip (the query rows per KV head set how many workgroups a split
+ * has), at least 128 keys per split, never a multiple of the 8 XCDs. */
 int mykfa_decode_num_splits(int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t seqlen_q,
                             int32_t capacity);
 /* Bytes of workspace mykfa_decode needs for this shape and split count. */

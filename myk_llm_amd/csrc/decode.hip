@@ -513,20 +513,21 @@ size_t decode_workspace_bytes(int batch, int num_heads, int seqlen_q, int head_d
 }
 
 int decode_default_splits(int batch, int num_heads, int num_kv_heads, int seqlen_q, int capacity) {
-    // Each split writes an fp32 partial row per query row that the merge reads back, so the
-    // keys per split grow with the query rows of a KV head: about 88 per row (352 for one query
-    // of a 4-head group, ~1400 for the 4-query draft), measured best on full 16K caches. Then at
+    // About 1400 keys per split: each split costs a workgroup prologue and an fp32 partial row
+    // per query row that the merge reads back, and longer splits stream longer runs of the cache.
+    // Measured on the 64 x 16K-cache batch, split-K + merge: 84.8 us at 12 splits (1366 keys)
+    // against 86.3 at 46 (352 keys) for one query, 91.2 at 12 for the 4-query draft. Then at
     // least ~512 workgroups (each kWaves KV-head units of one sequence) for short batches, at
     // least 128 keys per split, and never a multiple of the 8 XCDs: the workgroups of split s of
-    // every sequence would then all run on one XCD, idling the XCDs of the late splits.
+    // every sequence would then all run on one XCD, idling the XCDs of the late splits
+    // (measured: 8, 16, 32 or 64 splits 20-40 % slower than their neighbours).
     const long long kvh = num_kv_heads > 0 ? num_kv_heads : 1;
     const long long group = num_heads > 0 ? (num_heads + kvh - 1) / kvh : 1;
-    long long rows = group * (seqlen_q > 0 ? seqlen_q : 1);
+    const long long rows = group * (seqlen_q > 0 ? seqlen_q : 1);
     const long long row_tiles = (rows + 15) / 16;
-    rows = rows < 4 ? 4 : (rows > 16 ? 16 : rows);
     const long long pairs = (long long)(batch > 0 ? batch : 1) * ((kvh * row_tiles + kWaves - 1) / kWaves);
     const long long cap = capacity > 0 ? capacity : 1;
-    const long long chunk = 88 * rows;
+    const long long chunk = 1408;
     long long splits = (cap + chunk - 1) / chunk;
     const long long fill = (512 + pairs - 1) / pairs;
     if (splits < fill) splits = fill;

@@ -181,9 +181,9 @@ def test_decode_new_key_rules(L):
 
 
 def test_decode_split_heuristic(L):
-    # One query of a 4-head group over full 16K caches: ~352 keys per split (47, odd).
-    assert L.mykfa_decode_num_splits(64, 16, 4, 1, 16384) == 47
-    # The 4-query draft: 16 rows per KV head -> ~1408 keys per split, 12 splits.
+    # Full 16K caches of a 64-sequence batch: ~1408 keys per split, 12 splits, for one query of
+    # a 4-head group and for the 4-query draft alike.
+    assert L.mykfa_decode_num_splits(64, 16, 4, 1, 16384) == 12
     assert L.mykfa_decode_num_splits(64, 16, 4, 4, 16384) == 12
     # Never a multiple of the 8 XCDs; short caches are not split; bounds hold.
     # 8 sequences fill the chip only at 64 splits, capped at 4096 / 128 keys = 32, bumped to 33.
