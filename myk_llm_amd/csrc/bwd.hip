@@ -199,9 +199,11 @@ __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
 
     // K, V rows of this wave as B operands: lane holds K[nw0 + l32][16 kk + 8 g + i]. At
     // D <= 128 they are loaded after the ring's first tiles are issued, so the two latencies
-    // overlap: the compiler's own waits for these loads count only loads issued after them,
-    // and the older ring loads only lower the counter, so those waits stay exact. (At D = 256
-    // the compiler crashes on that order; there they load first and land before the ring.)
+    // overlap, and awaited (with those tiles) before the loop: the compiler places its own
+    // wait for a load issued before a loop at the load's first use inside it, where that
+    // wait would run every iteration and drain the ring's prefetched tile each time. (At
+    // D = 256 the compiler crashes on that order; there they load first and land before the
+    // ring.)
     s16x8 kop[KD], vop[KD];
     auto load_kv = [&]() {
         const int key = nw0 + l32;
@@ -333,7 +335,10 @@ __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
 #pragma unroll
     for (int t = 0; t < STAGES; ++t)
         if (t < iters) issue();
-    if constexpr (D <= 128) load_kv();
+    if constexpr (D <= 128) {
+        load_kv();
+        wait_vmcnt<0>();
+    }
 
     // dS: byte address of the current head's (pass-relative) first tile row of this sequence,
     // moved on by hpw heads per head change; the lane's 16-byte chunk within a block.

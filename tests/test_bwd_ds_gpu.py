@@ -72,6 +72,9 @@ CASES = [
     ("dense GQA8", [300], None, 8, 1, 128, (fa._UNBOUNDED, 0), True),
     ("dense GQA3", [190, 190], None, 6, 2, 128, (fa._UNBOUNDED, 0), True),
     ("dense GQA2 window", [260, 260], None, 4, 2, 128, (33, 0), True),
+    # Empty documents, documents shorter than a tile, and neighbours that share a 32-token
+    # stretch of the packed rows (their tiles must still get separate dS rows).
+    ("packed empty and tiny docs", [0, 5, 31, 0, 33, 64, 1, 0], None, 8, 2, 128, (fa._UNBOUNDED, 0), False),
 ]
 
 
