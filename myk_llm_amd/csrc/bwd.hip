@@ -533,6 +533,399 @@ __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
     }
 }
 
+// ---- 2b. dK / dV by wave pairs ----------------------------------------------------------
+//
+// Eight waves = four pairs. The two waves of pair p (waves p and p + 4, which the dispatcher
+// places on one SIMD) split a 32-key block's four products between them:
+//   wave A (0..3): K and the dV accumulator.  S = Q K^T, P = exp2(S c - lse), dV^T += dO^T P
+//   wave B (4..7): V and the dK accumulator.  dP = dO V^T, dS = P (dP - delta), dK^T += Q^T dS
+// P crosses from A to B through LDS in fp32, so dS is formed from the same fp32 P as in the
+// single-wave kernel above. Each wave holds half of that kernel's resident state (K and dV, or
+// V and dK: under 256 registers), so both waves of a pair share one SIMD and one's products run
+// while the other computes exponentials or waits for LDS. B works one query tile behind A: in
+// step t, A computes S(t), P(t) and dV(t) while B finishes dS(t-1) and dK(t-1) and computes
+// dP(t); one workgroup barrier per step publishes P(t) and the next ring tile.
+// The four pairs are HPW query heads x KPW = 4 / HPW consecutive 32-key blocks of one KV head.
+// The KPW pairs of a head share its (Q, dO, lse, delta) tile ring, streamed over the union of
+// their bands (a tile outside one pair's band is fully masked for it), which the A waves of
+// those pairs fill between them; every tile is read in the step that consumes it (B keeps its
+// transposed Q operands in registers for the next step), so a stage is refilled right after
+// the barrier that ends its step and a tile has STAGES - 1 steps to land. The HPW partial
+// sums of a key block are added through LDS in a fixed order: no atomics, bitwise repeatable.
+template <int D, int HPW, int STAGES, typename T, bool DS>
+__global__ __launch_bounds__(512) void bwd_dkdv_pair_kernel(BwdArgs a) {
+    constexpr int KPW = 4 / HPW;
+    constexpr int KD = D / 16;
+    constexpr int DB = D / 32;
+    constexpr int BMQ = 32;
+    constexpr int CPR = D / 8;
+    constexpr int QLOADS = BMQ * CPR / 64;          // 64-lane loads per 32 x D tile
+    constexpr int PARTS = KPW / 2;                  // A waves sharing one tensor's loads
+    constexpr int TLOADS = QLOADS / PARTS;          // tensor loads per issuing wave and tile
+    constexpr int LOADS = TLOADS + 1;               // + the lse or delta row
+    constexpr int TILE = BMQ * D;                   // elements of one 32 x D tile
+    constexpr int STAGE = 2 * TILE + 2 * BMQ * 2;   // Q, dO and 64 floats, in 16-bit units
+    constexpr int XBUF = 16 * 64;                   // floats of one pair's P exchange buffer
+    static_assert(HPW == 1 || HPW == 2, "two or four key blocks per workgroup");
+    static_assert(QLOADS % PARTS == 0, "tensor loads split evenly over the issuing waves");
+    static_assert(HPW == 1 || 2 * STAGES * STAGE * 2 >= 4 * DB * 16 * 64 * 4, "reduction fits the ring");
+    __shared__ __attribute__((aligned(16))) uint16_t ring_mem[HPW][STAGES][STAGE];
+    __shared__ __attribute__((aligned(16))) float xbuf[2][4][XBUF];
+
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int l32 = lane & 31, g = lane >> 5;
+    const bool role_b = wave >= 4;
+    const int pair = wave & 3;
+    const int hs = pair / KPW, kbi = pair % KPW;
+    // Key blocks are ranked from the END of each sequence (see bwd_dkdv_kernel).
+    const BlockCoord bc = block_coord(xcd_logical(blockIdx.x), a.gz, a.gy, a.cu_k != nullptr);
+    if (bc.rank >= a.gx) return;
+    const int kvh = a.kv0 + bc.group;
+    const int b = bc.seq;
+    SeqInfo ks = seq_info(b, a.cu_k, nullptr, a.seqlen_k, false);
+    const int k_len = ks.len;
+    const int kblk = bc.rank - (a.gx - (k_len + 32 * KPW - 1) / (32 * KPW));
+    if (kblk < 0) return;
+    const int n0 = kblk * 32 * KPW;
+    SeqInfo qs = seq_info(b, a.cu_q, nullptr, a.seqlen_q, false);
+    const int q_len = qs.len;
+    // Query i sees key j iff (i - j) in [q_len - k_len - wr, q_len - k_len + wl]
+    // (flash_attn.py:294-296); forward-oriented offsets for the element mask.
+    const int lo_t = band_lo(q_len, k_len, a.wr), hi_t = band_hi(q_len, k_len, a.wl);
+    const int lo_f = band_lo(k_len, q_len, a.wl), hi_f = band_hi(k_len, q_len, a.wr);
+    // The ring streams the union of the workgroup's bands; each pair masks by its own.
+    const int bsu = k_len - n0 < 32 * KPW ? k_len - n0 : 32 * KPW;  // >= 1
+    const Ranges ur = block_ranges(n0, bsu, lo_t, hi_t, q_len, BMQ);
+    const int ntiles = ur.hi > ur.lo ? (ur.hi - ur.lo + BMQ - 1) / BMQ : 0;
+    const int iters = ntiles * (a.group / HPW);
+    const int nw0 = n0 + 32 * kbi;
+    const int bs = k_len - nw0 < 32 ? k_len - nw0 : 32;
+    Ranges wr = {0, 0, 0, 0};
+    if (bs > 0) wr = block_ranges(nw0, bs, lo_t, hi_t, q_len, BMQ);
+    const int key = nw0 + l32;
+
+    uint16_t* const ring = &ring_mem[hs][0][0];
+    const uint32_t ring_lds = lds_addr(ring);
+    const int h0 = kvh * a.group + hs;  // first query head of this pair's ring
+    f32x16 acc[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
+    // K (wave A) or V (wave B) rows of this pair's keys as B operands: lane holds
+    // X[key][16 kk + 8 g + i]; rows past the sequence are 0.
+    s16x8 kv[KD];
+
+    if (!role_b) {
+        // ---- wave A: ring issue, S, P, dV ----
+        // This wave's share of each tile: tensor `tens` (0 = Q, 1 = dO), loads
+        // [part * TLOADS, (part + 1) * TLOADS) of it, and the lse (even kbi) or delta row.
+        const int tens = kbi / PARTS, part = kbi % PARTS;
+        const bool f_delta = (kbi & 1) != 0;
+        const int64_t tstride = tens == 0 ? a.qts : a.dots;
+        const int64_t thead = tens == 0 ? a.qhs : a.dohs;
+        const uint16_t* tbase = tens == 0 ? a.q + (int64_t)b * a.qbs + qs.tok0 * a.qts
+                                          : a.dout + (int64_t)b * a.dobs + qs.tok0 * a.dots;
+        const float* fbase = (f_delta ? a.delta : a.lse) + qs.row0;
+        unsigned t_lane[TLOADS];
+#pragma unroll
+        for (int j = 0; j < TLOADS; ++j) {
+            const int p = (part * TLOADS + j) * 64 + lane;
+            const int row = p / CPR, logical = (p % CPR) ^ lds_swz<D>(row);
+            t_lane[j] = (unsigned)(row * (int)(tstride * 2) + logical * 16);
+        }
+        const unsigned f_lane = (unsigned)(lane * 4);
+        const uint32_t t_lds = (uint32_t)(tens * TILE * 2 + part * TLOADS * 1024);
+        const uint32_t f_lds = (uint32_t)(2 * TILE * 2 + (f_delta ? BMQ * 4 : 0));
+        // Issue-side state, advanced by additions: the next tile's first-row address and the
+        // bytes from it to the end of the sequence's rows (rows at or beyond q_len read 0);
+        // after ntiles tiles both move to the next head of this ring (HPW heads on).
+        const int rows0 = q_len - ur.lo;  // >= 1 whenever a tile is issued
+        const int tb0 = rows0 > 0 ? (int)(((int64_t)(rows0 - 1) * tstride + D) * 2) : 0;
+        const int fb0 = rows0 * 4;
+        const uint64_t t_tstep = (uint64_t)(BMQ * tstride) * 2;
+        const uint64_t t_hb = (uint64_t)(HPW * thead) * 2, f_hb = (uint64_t)(HPW * a.lse_hs) * 4;
+        uint64_t ht = reinterpret_cast<uint64_t>(tbase + (int64_t)h0 * thead + (int64_t)ur.lo * tstride);
+        uint64_t hf = reinterpret_cast<uint64_t>(fbase + (int64_t)h0 * a.lse_hs + ur.lo);
+        uint64_t tt = ht, tf = hf;
+        int tb = tb0, fb = fb0, iss_tile = 0, iss_stage = 0;
+        // A tile's loads go out in three chunks spread over the step (loads [J0, J1) of the
+        // tensor, then the lse / delta row): issued back to back, the four A waves' loads
+        // queue up in the CU's memory pipe and stall their waves for hundreds of cycles.
+        auto issue_part = [&](auto J0c, auto J1c, bool with_f) {
+            constexpr int J0 = decltype(J0c)::value, J1 = decltype(J1c)::value;
+            const uint32_t st = ring_lds + iss_stage * (STAGE * 2);
+            const i32x4 rt = buffer_rsrc32(tt, tb);
+#pragma unroll
+            for (int j = J0; j < J1; ++j) dma16(rt, st + t_lds + j * 1024, t_lane[j]);
+            if (with_f && lane < 32) dma4(buffer_rsrc32(tf, fb), st + f_lds, f_lane);
+        };
+        auto issue_end = [&]() {
+            iss_stage = iss_stage + 1 == STAGES ? 0 : iss_stage + 1;
+            if (++iss_tile == ntiles) {
+                iss_tile = 0;
+                ht += t_hb;
+                hf += f_hb;
+                tt = ht;
+                tf = hf;
+                tb = tb0;
+                fb = fb0;
+            } else {
+                tt += t_tstep;
+                tf += BMQ * 4;
+                tb -= (int)t_tstep;
+                fb -= BMQ * 4;
+            }
+        };
+        using C0 = std::integral_constant<int, 0>;
+        using C1 = std::integral_constant<int, TLOADS / 3>;
+        using C2 = std::integral_constant<int, 2 * TLOADS / 3>;
+        using C3 = std::integral_constant<int, TLOADS>;
+#pragma unroll
+        for (int t = 0; t < STAGES - 1; ++t)
+            if (t < iters) {
+                issue_part(C0{}, C3{}, true);
+                issue_end();
+            }
+        {
+            const uint16_t* kp = a.k + (int64_t)b * a.kbs + (ks.tok0 + key) * a.kts + (int64_t)kvh * a.khs;
+#pragma unroll
+            for (int kk = 0; kk < KD; ++kk) {
+                const s16x8 z = {0, 0, 0, 0, 0, 0, 0, 0};
+                kv[kk] = key < k_len ? ld16(kp + 16 * kk + 8 * g) : z;
+            }
+        }
+        wait_vmcnt<0>();
+        barrier_lds();
+
+        const float qk_scale = sgpr_copy(a.qk_scale);
+        int cur_tile = 0, cur_stage = 0;
+        for (int it = 0; it < iters; ++it) {
+            // Tile it + STAGES - 1 goes into the stage tile it - 1 used, in three chunks.
+            const bool refill = it + STAGES - 1 < iters;
+            if (refill) issue_part(C0{}, C1{}, false);
+            const int m0 = ur.lo + cur_tile * BMQ;
+            const bool masked = !(m0 >= wr.mid_lo && m0 + BMQ <= wr.mid_hi);
+            const uint16_t* Qs = ring + cur_stage * STAGE;
+            const uint16_t* DOs = Qs + TILE;
+            const float* fl = reinterpret_cast<const float*>(Qs + 2 * TILE);
+            cur_tile = cur_tile + 1 == ntiles ? 0 : cur_tile + 1;
+            cur_stage = cur_stage + 1 == STAGES ? 0 : cur_stage + 1;
+            // All operand reads of a product are issued before it (the compiler would otherwise
+            // serialize read -> wait -> product): the Q rows and the lse row for S, then the
+            // transposed dO operands of dV, whose latency hides under the exponentials.
+            s16x8 qa[KD];
+#pragma unroll
+            for (int kk = 0; kk < KD; ++kk) qa[kk] = lds_row_op<D>(Qs, 0, l32, g, kk);
+            f32x4 lq[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) lq[c] = *reinterpret_cast<const f32x4*>(fl + 16 * (c >> 1) + 8 * g + 4 * (c & 1));
+            __builtin_amdgcn_sched_barrier(0);
+            // S = Q K^T: lane column = key, register r = 8 kb + i holds row m0 + 16 kb + 8 g + i.
+            f32x16 s;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s[r] = 0.f;
+#pragma unroll
+            for (int kk = 0; kk < KD; ++kk) s = T::mfma32(qa[kk], kv[kk], s);
+            s16x8 dot[DB][2];
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) dot[db][kb] = lds_tr_op<D>(DOs, db, kb, lane);
+            if (refill) issue_part(C1{}, C2{}, false);
+            __builtin_amdgcn_sched_barrier(0);
+            float pv[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) pv[r] = fast_exp2(fmaf(s[r], qk_scale, -lq[r >> 2][r & 3]));
+            // Band mask on tiles that are not wholly inside this pair's band: query i is
+            // visible from this lane's key iff lo_f <= key - i <= hi_f, i < q_len, key < k_len.
+            if (masked) mask_runs16(pv, m0 + 8 * g, key - hi_f, key < k_len ? min(key - lo_f, q_len - 1) : key - hi_f - 1);
+            // P for wave B, in chunk-major lane order (16-byte writes, conflict-free).
+            float* xp = &xbuf[it & 1][pair][0];
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                *reinterpret_cast<f32x4*>(xp + c * 256 + lane * 4) =
+                    f32x4{pv[4 * c], pv[4 * c + 1], pv[4 * c + 2], pv[4 * c + 3]};
+            s16x8 pb[2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const float* pk = pv + 8 * kb;
+                u32x4 pw = {T::pack2(pk[0], pk[1]), T::pack2(pk[2], pk[3]), T::pack2(pk[4], pk[5]), T::pack2(pk[6], pk[7])};
+                pb[kb] = __builtin_bit_cast(s16x8, pw);
+            }
+            // dV^T += dO^T P.
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) acc[db] = T::mfma32(dot[db][kb], pb[kb], acc[db]);
+            if (refill) {
+                issue_part(C2{}, C3{}, true);
+                issue_end();
+            }
+            // Tile it + 1 landed (this wave's loads of it); later tiles may stay in flight.
+            const int after = iters - 2 - it < STAGES - 2 ? iters - 2 - it : STAGES - 2;
+            if (after >= 0) ring_wait<LOADS, STAGES>(after);
+            barrier_lds();
+        }
+    } else {
+        // ---- wave B: dP, dS, dK (one tile behind A) ----
+        {
+            const uint16_t* vp = a.v + (int64_t)b * a.vbs + (ks.tok0 + key) * a.vts + (int64_t)kvh * a.vhs;
+#pragma unroll
+            for (int kk = 0; kk < KD; ++kk) {
+                const s16x8 z = {0, 0, 0, 0, 0, 0, 0, 0};
+                kv[kk] = key < k_len ? ld16(vp + 16 * kk + 8 * g) : z;
+            }
+        }
+        wait_vmcnt<0>();
+        barrier_lds();
+
+        // dS rows of this pair's first head (pass-relative) in the sequence; moved on by HPW
+        // heads per head change.
+        uint64_t ds_ptr = 0, ds_hstep = 0;
+        int ds_w = 0, ds_rows = 0;
+        if constexpr (DS) {
+            const int t0 = ds_tile_base(b, qs.tok0, a.seqlen_q, a.cu_q != nullptr);
+            ds_w = sgpr_copy(a.ds_w);
+            ds_rows = sgpr_copy(a.ds_nqt) - t0;
+            ds_hstep = (uint64_t)HPW * (uint64_t)a.ds_hs * 2;
+            ds_ptr = reinterpret_cast<uint64_t>(a.ds) +
+                     ((uint64_t)((int64_t)(kvh - a.kv0) * a.group + hs) * (uint64_t)a.ds_hs + (uint64_t)t0 * ds_w * 1024) * 2;
+        }
+        const int ds_jblk = nw0 >> 5, ds_lob = lo_f >> 5;
+        const unsigned ds_lane = (unsigned)(l32 * 64 + 16 * g);
+        const bool zero_keys = bs < 32 && key >= k_len;
+        // dS(t) = P(t) (dP(t) - delta(t)) and dK^T += Q^T dS for the tile of the previous step,
+        // whose dP - delta and transposed Q operands this wave kept in registers.
+        f32x16 dpm;
+        s16x8 qt[DB][2];
+        int pm0 = 0;
+        uint64_t pds = 0;
+        auto read_p = [&](int pit, f32x4* x) {
+            const float* xp = &xbuf[pit & 1][pair][0];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) x[c] = *reinterpret_cast<const f32x4*>(xp + c * 256 + lane * 4);
+        };
+        auto finish = [&](const f32x4* px) {
+            float pv[16];
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) pv[4 * c + e] = px[c][e];
+            s16x8 dsb[2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                float dsv[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) dsv[i] = pv[8 * kb + i] * dpm[8 * kb + i];
+                u32x4 dw = {T::pack2(dsv[0], dsv[1]), T::pack2(dsv[2], dsv[3]), T::pack2(dsv[4], dsv[5]),
+                            T::pack2(dsv[6], dsv[7])};
+                dsb[kb] = __builtin_bit_cast(s16x8, dw);
+            }
+            if constexpr (DS) {
+                // Block (tile pm0 / 32, key block nw0 / 32), stored only for tiles of this
+                // pair's own band: the set the dS-driven dQ pass reads. Lane (key l32, g)
+                // holds queries 16 kb + 8 g + 0..7 of its key; keys past the sequence as 0.
+                const int ti = pm0 >> 5;
+                const int slot = ds_jblk - max(ti + ds_lob, 0);  // ds_first_block(ti, lo_f)
+                if (pm0 >= wr.lo && pm0 < wr.hi && slot >= 0 && slot < ds_w && ti < ds_rows) {
+                    gs16x8* dsp = reinterpret_cast<gs16x8*>(pds + (uint64_t)(ti * ds_w + slot) * 2048 + ds_lane);
+                    const s16x8 z = {0, 0, 0, 0, 0, 0, 0, 0};
+                    dsp[0] = zero_keys ? z : dsb[0];
+                    dsp[2] = zero_keys ? z : dsb[1];
+                }
+            }
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) acc[db] = T::mfma32(qt[db][kb], dsb[kb], acc[db]);
+        };
+        int cur_tile = 0, cur_stage = 0;
+        for (int it = 0; it < iters; ++it) {
+            const int m0 = ur.lo + cur_tile * BMQ;
+            const uint16_t* Qs = ring + cur_stage * STAGE;
+            const uint16_t* DOs = Qs + TILE;
+            const float* fl = reinterpret_cast<const float*>(Qs + 2 * TILE);
+            // Operand reads first (see wave A): P of the previous tile, this tile's dO rows
+            // and delta row.
+            f32x4 px[4];
+            if (it > 0) read_p(it - 1, px);
+            s16x8 oa[KD];
+#pragma unroll
+            for (int kk = 0; kk < KD; ++kk) oa[kk] = lds_row_op<D>(DOs, 0, l32, g, kk);
+            f32x4 dl[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) dl[c] = *reinterpret_cast<const f32x4*>(fl + 32 + 16 * (c >> 1) + 8 * g + 4 * (c & 1));
+            __builtin_amdgcn_sched_barrier(0);
+            if (it > 0) finish(px);
+            __builtin_amdgcn_sched_barrier(0);
+            pm0 = m0;
+            pds = ds_ptr;
+            if (cur_tile + 1 == ntiles) ds_ptr += ds_hstep;
+            cur_tile = cur_tile + 1 == ntiles ? 0 : cur_tile + 1;
+            cur_stage = cur_stage + 1 == STAGES ? 0 : cur_stage + 1;
+            // Q^T operands of this tile's dK product (kept for the next step), issued after the
+            // previous tile's dK products have taken theirs.
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) qt[db][kb] = lds_tr_op<D>(Qs, db, kb, lane);
+            // dP = dO V^T, then dP - delta in place.
+            f32x16 dp;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) dp[r] = 0.f;
+#pragma unroll
+            for (int kk = 0; kk < KD; ++kk) dp = T::mfma32(oa[kk], kv[kk], dp);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) dpm[r] = dp[r] - dl[r >> 2][r & 3];
+            barrier_lds();
+        }
+        if (iters > 0) {
+            f32x4 px[4];
+            read_p(iters - 1, px);
+            finish(px);
+        }
+    }
+
+    // Sum the two head slots' partials of each key block in a fixed order (slot 1 into 0).
+    if constexpr (HPW == 2) {
+        float* red = reinterpret_cast<float*>(&ring_mem[0][0][0]);
+        constexpr int PART = DB * 16 * 64;
+        float* part_buf = red + ((role_b ? 2 : 0) + kbi) * PART;
+        __syncthreads();
+        if (hs == 1) {
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) part_buf[(db * 16 + r) * 64 + lane] = acc[db][r];
+        }
+        __syncthreads();
+        if (hs == 0) {
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[db][r] += part_buf[(db * 16 + r) * 64 + lane];
+        }
+    }
+
+    // Store dK * sm_scale (wave B) or dV (wave A) (flash_attn.py:312-314); lane column = key,
+    // registers = d.
+    if (hs == 0 && bs > 0 && key < k_len) {
+        const float sc = role_b ? a.sm_scale : 1.0f;
+        uint16_t* const outp = role_b ? a.dk + (int64_t)b * a.dkbs + (ks.tok0 + key) * a.dkts + (int64_t)kvh * a.dkhs
+                                      : a.dv + (int64_t)b * a.dvbs + (ks.tok0 + key) * a.dvts + (int64_t)kvh * a.dvhs;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int rq = 0; rq < 4; ++rq) {
+                const int d0 = 32 * db + 8 * rq + 4 * g;
+                u32x2 w = {T::pack2(acc[db][4 * rq] * sc, acc[db][4 * rq + 1] * sc),
+                           T::pack2(acc[db][4 * rq + 2] * sc, acc[db][4 * rq + 3] * sc)};
+                *reinterpret_cast<u32x2*>(outp + d0) = w;
+            }
+    }
+}
+
 // ---- 3. dQ ------------------------------------------------------------------------------
 
 template <int D, int BN, int NW, int STAGES, typename T>
@@ -982,13 +1375,44 @@ hipError_t dkdv_launch(BwdArgs a, int num_kv_heads, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Wave-pair dK/dV: HPW = 2 query heads x 2 key blocks per workgroup when the GQA group is
+// even, else 1 head x 4 key blocks.
+template <int D, int HPW, int STAGES, typename T, bool DS>
+hipError_t dkdv_pair_launch_hpw(BwdArgs a, int num_kv_heads, hipStream_t s) {
+    a.hpw = HPW;
+    const int keys_per_wg = 32 * (4 / HPW);
+    a.gx = (a.seqlen_k + keys_per_wg - 1) / keys_per_wg;
+    a.gy = a.batch;
+    a.gz = num_kv_heads;
+    const long long n = block_grid_size(a.gx, a.gz, a.gy, a.cu_k != nullptr);
+    if (n == 0) return hipSuccess;
+    if (n > (1LL << 30)) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL((bwd_dkdv_pair_kernel<D, HPW, STAGES, T, DS>), dim3(xcd_grid((int)n)), dim3(512), 0, s, a);
+    return hipGetLastError();
+}
+template <int D, typename T, bool DS = false>
+hipError_t dkdv_pair_launch(const BwdArgs& a, int num_kv_heads, hipStream_t s) {
+    if (a.group % 2 == 0) return dkdv_pair_launch_hpw<D, 2, D == 128 ? 3 : 4, T, DS>(a, num_kv_heads, s);
+    return dkdv_pair_launch_hpw<D, 1, 4, T, DS>(a, num_kv_heads, s);
+}
+// MYKFA_DKDV_PAIR=0 selects the single-wave dK/dV kernel at head_dim 128 (for comparisons).
+bool dkdv_pair_enabled() {
+    static const bool on = [] {
+        const char* e = getenv("MYKFA_DKDV_PAIR");
+        return e == nullptr || e[0] != '0';
+    }();
+    return on;
+}
+
 template <typename T>
 hipError_t dkdv_dtype(const BwdArgs& a, int D, int num_kv_heads, hipStream_t s) {
     switch (D) {
         case 16: return dkdv_launch<16, 4, 3, T>(a, num_kv_heads, s);
         case 32: return dkdv_launch<32, 4, 3, T>(a, num_kv_heads, s);
         case 64: return dkdv_launch<64, 4, 2, T>(a, num_kv_heads, s);
-        case 128: return dkdv_launch<128, 4, 2, T>(a, num_kv_heads, s);
+        case 128:
+            if (dkdv_pair_enabled()) return dkdv_pair_launch<128, T>(a, num_kv_heads, s);
+            return dkdv_launch<128, 4, 2, T>(a, num_kv_heads, s);
         case 256: return dkdv_launch<256, 2, 2, T>(a, num_kv_heads, s);
         default: return hipErrorInvalidValue;
     }
@@ -1045,7 +1469,7 @@ hipError_t ds_passes(BwdArgs a, const mykfa_bwd_params& p, int kv_per_pass, hipS
         // dQ: 64 keys per step, 3 stages (144 KB of LDS: one workgroup per CU) measured best
         // among 32 / 64 keys per step and 2-6 stages (the single-workgroup ring holds the most
         // bytes in flight).
-        e = dkdv_launch<128, 4, 2, T, true>(a, n, s);
+        e = dkdv_pair_enabled() ? dkdv_pair_launch<128, T, true>(a, n, s) : dkdv_launch<128, 4, 2, T, true>(a, n, s);
         if (e == hipSuccess) e = dq_ds_launch<128, 4, 2, 3, T>(a, n, s);
     }
     return e;
@@ -1093,9 +1517,13 @@ hipError_t launch_bwd_ds(const mykfa_bwd_params& p, void* ws, int kv_per_pass, h
 hipError_t launch_bwd_ds_half(const mykfa_bwd_params& p, void* ws, bool dq, hipStream_t stream) {
     const BwdArgs a = ds_args(p, ws);
     const int n = p.fwd.num_kv_heads;
-    if (p.fwd.dtype == MYKFA_BF16)
-        return dq ? dq_ds_launch<128, 4, 2, 3, BF16>(a, n, stream) : dkdv_launch<128, 4, 2, BF16, true>(a, n, stream);
-    return dq ? dq_ds_launch<128, 4, 2, 3, FP16>(a, n, stream) : dkdv_launch<128, 4, 2, FP16, true>(a, n, stream);
+    const bool pair = dkdv_pair_enabled();
+    if (p.fwd.dtype == MYKFA_BF16) {
+        if (dq) return dq_ds_launch<128, 4, 2, 3, BF16>(a, n, stream);
+        return pair ? dkdv_pair_launch<128, BF16, true>(a, n, stream) : dkdv_launch<128, 4, 2, BF16, true>(a, n, stream);
+    }
+    if (dq) return dq_ds_launch<128, 4, 2, 3, FP16>(a, n, stream);
+    return pair ? dkdv_pair_launch<128, FP16, true>(a, n, stream) : dkdv_launch<128, 4, 2, FP16, true>(a, n, stream);
 }
 
 hipError_t launch_bwd_preprocess(const mykfa_bwd_params& p, hipStream_t stream) {

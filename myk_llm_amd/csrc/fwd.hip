@@ -147,19 +147,47 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdArgs a) {
         const bool masked = !(n0 >= wr.mid_lo && n0 + BN <= wr.mid_hi);
         const uint16_t* Ks = smem[t % STAGES][0];
         const uint16_t* Vs = smem[t % STAGES][1];
-        // S^T = K Q^T (raw scores), 32 keys per block.
+        // S^T = K Q^T (raw scores), 32 keys per block. Every K operand read is issued before the
+        // products (left to itself the compiler reuses one register quad: read, wait, product,
+        // read again, exposing the LDS latency once per product), and the two blocks'
+        // accumulation chains alternate.
         f32x16 st[NB];
+        s16x8 kop[NB][KD];
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) st[nb][r] = 0.f;
             const int row = nb * 32 + perm32(l32);
 #pragma unroll
-            for (int kk = 0; kk < KD; ++kk) {
-                s16x8 kop = *reinterpret_cast<const s16x8*>(Ks + row * D + (((2 * kk + g) ^ lds_swz<D>(row)) << 3));
-                st[nb] = T::mfma32(kop, qop[kk], st[nb]);
+            for (int kk = 0; kk < KD; ++kk)
+                kop[nb][kk] = *reinterpret_cast<const s16x8*>(Ks + row * D + (((2 * kk + g) ^ lds_swz<D>(row)) << 3));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) st[nb][r] = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < KD; ++kk)
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) st[nb] = T::mfma32(kop[nb][kk], qop[kk], st[nb]);
+        // V^T operands of O^T += V^T P^T through the LDS transpose read, issued now so that
+        // they land while the softmax runs.
+        const int G = lane >> 4, jj = lane & 15;
+        s16x8 vop[DB][KB];
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+            int col = 32 * db + 16 * (G & 1) + 4 * (jj & 3);
+            const bool dvalid = col < D;
+            if (!dvalid) col = col % D;
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+                const int row = 16 * kb + 8 * (G >> 1) + (jj >> 2);
+                s16x4 lo4 = ds_read_tr(Vs + lds_off<D>(row, col));
+                s16x4 hi4 = ds_read_tr(Vs + lds_off<D>(row + 4, col));
+                vop[db][kb] = cat4(lo4, hi4);
+                if (!dvalid) vop[db][kb] = s16x8{0, 0, 0, 0, 0, 0, 0, 0};
             }
         }
+        __builtin_amdgcn_sched_barrier(0);
         // Band mask, only on tiles that cross the band edge (flash_attn.py:140-145).
         // Key j is visible from this lane's query iff lo_off <= j - qi <= hi_off and j < k_len:
         // one range (register r of block nb holds key n0 + 32 nb + out_row32(r, g)); masked
@@ -214,23 +242,11 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdArgs a) {
                 u32x4 wv = {w[0], w[1], w[2], w[3]};
                 pop[nb * 2 + half] = __builtin_bit_cast(s16x8, wv);
             }
-        // O^T += V^T P^T; V^T operand through the LDS transpose read.
-        const int G = lane >> 4, jj = lane & 15;
+        // O^T += V^T P^T.
 #pragma unroll
-        for (int db = 0; db < DB; ++db) {
-            int col = 32 * db + 16 * (G & 1) + 4 * (jj & 3);
-            const bool dvalid = col < D;
-            if (!dvalid) col = col % D;
+        for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-            for (int kb = 0; kb < KB; ++kb) {
-                const int row = 16 * kb + 8 * (G >> 1) + (jj >> 2);
-                s16x4 lo4 = ds_read_tr(Vs + lds_off<D>(row, col));
-                s16x4 hi4 = ds_read_tr(Vs + lds_off<D>(row + 4, col));
-                s16x8 vop = cat4(lo4, hi4);
-                if (!dvalid) vop = s16x8{0, 0, 0, 0, 0, 0, 0, 0};
-                acc[db] = T::mfma32(vop, pop[kb], acc[db]);
-            }
-        }
+            for (int db = 0; db < DB; ++db) acc[db] = T::mfma32(vop[db][kb], pop[kb], acc[db]);
     }
 
     if (bs <= 0) return;
