@@ -75,6 +75,14 @@ __device__ inline int ds_tile_base(int b, int64_t tok0, int seqlen_q, bool varle
     return varlen ? (int)(tok0 >> 5) + b : b * ((seqlen_q + 31) >> 5);
 }
 
+// Layout of one stored 32 x 32 dS block (bf16, 2 KB): two 1 KB halves by query half
+// kb = q / 16; in half kb the 16-byte chunk ds_chunk(kb, g, key) holds queries
+// 16 kb + 8 g + 0..7 of key `key`. A dK/dV wave holds exactly these 8 values per lane and
+// register group (lane = key + 32 g), so each of its two stores writes 1 KB contiguously
+// (16 full cache lines); the XOR places the 16 chunks that one 32-lane transpose read of the
+// dQ pass touches (keys r..r+3 x both g x both kb) on distinct banks.
+__device__ inline int ds_chunk(int kb, int g, int key) { return 64 * kb + 32 * g + (key ^ (4 * (2 * kb + g))); }
+
 // ---- 1. delta = rowsum(dO * O) ---------------------------------------------------------
 
 // One flat grid over the (row, head) items: rows run over the packed tokens (varlen:
@@ -152,7 +160,7 @@ __device__ inline s16x8 lds_tr_op(const uint16_t* tile, int db, int kb, int lane
 // tiles through a wave-private asynchronous LDS ring: the main loop has no workgroup
 // barrier. The hpw partial dK/dV of a key block are summed through LDS in a fixed order
 // (deterministic) at the end. With DS, every 32 x 32 dS block is also stored (bf16, the
-// rounding its dV/dK product uses) for the dS-driven dQ pass: key-major, 32 queries per key.
+// rounding its dV/dK product uses) for the dS-driven dQ pass, in the ds_chunk layout.
 template <int D, int NW, int STAGES, typename T, bool DS>
 __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
     constexpr int KD = D / 16;
@@ -354,7 +362,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
         ds_jblk = nw0 >> 5;
         ds_lob = lo_f >> 5;
     }
-    const unsigned ds_lane = (unsigned)(l32 * 64 + 16 * g);
+    const unsigned ds_lane0 = (unsigned)(ds_chunk(0, g, l32) * 16), ds_lane1 = (unsigned)(ds_chunk(1, g, l32) * 16);
     const bool partial_block = bs < 32;
     // A tile's dS block is stored at the top of the NEXT iteration, right after its ring wait:
     // stores share the vector memory counter with the ring loads, and a store issued before
@@ -366,9 +374,8 @@ __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
         if (ds_keep_ok) {
             // Global (not generic) address space: a flat store would also count against the
             // LDS counter and hold up every LDS wait until it completed.
-            gs16x8* dsp = reinterpret_cast<gs16x8*>(ds_keep_at + ds_lane);
-            dsp[0] = ds_keep[0];
-            dsp[2] = ds_keep[1];
+            *reinterpret_cast<gs16x8*>(ds_keep_at + ds_lane0) = ds_keep[0];
+            *reinterpret_cast<gs16x8*>(ds_keep_at + ds_lane1) = ds_keep[1];
         }
         ds_keep_ok = false;
     };
@@ -793,7 +800,7 @@ __global__ __launch_bounds__(512) void bwd_dkdv_pair_kernel(BwdArgs a) {
                      ((uint64_t)((int64_t)(kvh - a.kv0) * a.group + hs) * (uint64_t)a.ds_hs + (uint64_t)t0 * ds_w * 1024) * 2;
         }
         const int ds_jblk = nw0 >> 5, ds_lob = lo_f >> 5;
-        const unsigned ds_lane = (unsigned)(l32 * 64 + 16 * g);
+        const unsigned ds_lane0 = (unsigned)(ds_chunk(0, g, l32) * 16), ds_lane1 = (unsigned)(ds_chunk(1, g, l32) * 16);
         const bool zero_keys = bs < 32 && key >= k_len;
         // dS(t) = P(t) (dP(t) - delta(t)) and dK^T += Q^T dS for the tile of the previous step,
         // whose dP - delta and transposed Q operands this wave kept in registers.
@@ -825,14 +832,17 @@ __global__ __launch_bounds__(512) void bwd_dkdv_pair_kernel(BwdArgs a) {
             if constexpr (DS) {
                 // Block (tile pm0 / 32, key block nw0 / 32), stored only for tiles of this
                 // pair's own band: the set the dS-driven dQ pass reads. Lane (key l32, g)
-                // holds queries 16 kb + 8 g + 0..7 of its key; keys past the sequence as 0.
+                // holds queries 16 kb + 8 g + 0..7 of its key (chunk ds_chunk(kb, g, l32));
+                // keys past the sequence as 0.
                 const int ti = pm0 >> 5;
                 const int slot = ds_jblk - max(ti + ds_lob, 0);  // ds_first_block(ti, lo_f)
                 if (pm0 >= wr.lo && pm0 < wr.hi && slot >= 0 && slot < ds_w && ti < ds_rows) {
-                    gs16x8* dsp = reinterpret_cast<gs16x8*>(pds + (uint64_t)(ti * ds_w + slot) * 2048 + ds_lane);
+                    const uint64_t blk = pds + (uint64_t)(ti * ds_w + slot) * 2048;
                     const s16x8 z = {0, 0, 0, 0, 0, 0, 0, 0};
-                    dsp[0] = zero_keys ? z : dsb[0];
-                    dsp[2] = zero_keys ? z : dsb[1];
+                    // Non-temporal: the dQ pass reads them long after; kept out of the way
+                    // of the Q / dO tiles other workgroups reuse through L2 (445 -> 434 us).
+                    __builtin_nontemporal_store(zero_keys ? z : dsb[0], reinterpret_cast<gs16x8*>(blk + ds_lane0));
+                    __builtin_nontemporal_store(zero_keys ? z : dsb[1], reinterpret_cast<gs16x8*>(blk + ds_lane1));
                 }
             }
 #pragma unroll
@@ -1122,14 +1132,14 @@ __global__ __launch_bounds__(NW * 64) void bwd_dq_kernel(BwdArgs a) {
 
 // ---- 4. dQ from the stored dS ------------------------------------------------------------
 
-// B operand (16 keys x 32 queries) of a 32 x 32 dS block stored key-major in LDS (32 queries
-// per 64-byte row, unswizzled): lane holds blk[16 kb + 8 g + i][l32], i = 0..7, by two
-// transpose reads (4 rows x 16 columns per 16-lane group each).
+// B operand (16 keys x 32 queries) of a 32 x 32 dS block in the ds_chunk layout in LDS: lane
+// holds blk[key 16 kb + 8 g + i][query l32], i = 0..7, by two transpose reads (each 16-lane
+// group: 4 keys x 16 queries, 4 consecutive queries of one key per lane).
 __device__ inline s16x8 lds_tr_block32(const uint16_t* blk, int kb, int lane) {
     const int G = lane >> 4, jj = lane & 15;
-    const int col = 16 * (G & 1) + 4 * (jj & 3);
-    const int row = 16 * kb + 8 * (G >> 1) + (jj >> 2);
-    return cat4(ds_read_tr(blk + row * 32 + col), ds_read_tr(blk + (row + 4) * 32 + col));
+    const int key = 16 * kb + 8 * (G >> 1) + (jj >> 2);
+    const int qk = G & 1, qg = (jj >> 1) & 1, half = 4 * (jj & 1);
+    return cat4(ds_read_tr(blk + ds_chunk(qk, qg, key) * 8 + half), ds_read_tr(blk + ds_chunk(qk, qg, key + 4) * 8 + half));
 }
 
 // dQ = sm_scale * dS K over the band from the dS blocks the dK/dV pass stored: one product per
@@ -1392,10 +1402,12 @@ hipError_t dkdv_pair_launch_hpw(BwdArgs a, int num_kv_heads, hipStream_t s) {
 }
 template <int D, typename T, bool DS = false>
 hipError_t dkdv_pair_launch(const BwdArgs& a, int num_kv_heads, hipStream_t s) {
-    if (a.group % 2 == 0) return dkdv_pair_launch_hpw<D, 2, D == 128 ? 3 : 4, T, DS>(a, num_kv_heads, s);
+    if (a.group % 2 == 0) return dkdv_pair_launch_hpw<D, 2, 3, T, DS>(a, num_kv_heads, s);
     return dkdv_pair_launch_hpw<D, 1, 4, T, DS>(a, num_kv_heads, s);
 }
-// MYKFA_DKDV_PAIR=0 selects the single-wave dK/dV kernel at head_dim 128 (for comparisons).
+// MYKFA_DKDV_PAIR=0 selects the single-wave dK/dV kernel at head_dim 128 (for comparisons; at
+// head_dim 64 the single-wave kernel is the faster one: cfg2 dK/dV 63.9 us against 83.5 us for
+// the pair kernel, whose per-step exchange and barrier do not shrink with D).
 bool dkdv_pair_enabled() {
     static const bool on = [] {
         const char* e = getenv("MYKFA_DKDV_PAIR");
@@ -1403,7 +1415,6 @@ bool dkdv_pair_enabled() {
     }();
     return on;
 }
-
 template <typename T>
 hipError_t dkdv_dtype(const BwdArgs& a, int D, int num_kv_heads, hipStream_t s) {
     switch (D) {
