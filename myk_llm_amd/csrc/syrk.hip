@@ -121,14 +121,23 @@ __global__ __launch_bounds__(kNW * 64) void syrk_kernel(mykfa_syrk_params p, int
         if (kt + kStages - 1 < nk) issue(kt + kStages - 1);
         const uint16_t* As = smem[kt % kStages][0];
         const uint16_t* Bs = smem[kt % kStages][1];
+        // Every operand of the stage is read before its products: left to itself the compiler
+        // reads, waits and multiplies one k-step at a time, exposing the LDS latency per step.
+        s16x8 av[kBK / 16][2], bv[kBK / 16][2];
 #pragma unroll
         for (int kk = 0; kk < kBK / 16; ++kk) {
-            const s16x8 a0 = panel_op(As, wm * 64, l32, g, kk), a1 = panel_op(As, wm * 64 + 32, l32, g, kk);
-            const s16x8 b0 = panel_op(Bs, wn * 64, l32, g, kk), b1 = panel_op(Bs, wn * 64 + 32, l32, g, kk);
-            acc[0][0] = BF16::mfma32(a0, b0, acc[0][0]);
-            acc[0][1] = BF16::mfma32(a0, b1, acc[0][1]);
-            acc[1][0] = BF16::mfma32(a1, b0, acc[1][0]);
-            acc[1][1] = BF16::mfma32(a1, b1, acc[1][1]);
+            av[kk][0] = panel_op(As, wm * 64, l32, g, kk);
+            av[kk][1] = panel_op(As, wm * 64 + 32, l32, g, kk);
+            bv[kk][0] = panel_op(Bs, wn * 64, l32, g, kk);
+            bv[kk][1] = panel_op(Bs, wn * 64 + 32, l32, g, kk);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int kk = 0; kk < kBK / 16; ++kk) {
+            acc[0][0] = BF16::mfma32(av[kk][0], bv[kk][0], acc[0][0]);
+            acc[0][1] = BF16::mfma32(av[kk][0], bv[kk][1], acc[0][1]);
+            acc[1][0] = BF16::mfma32(av[kk][1], bv[kk][0], acc[1][0]);
+            acc[1][1] = BF16::mfma32(av[kk][1], bv[kk][1], acc[1][1]);
         }
     }
 
