@@ -326,7 +326,9 @@ int mykfa_bwd(const mykfa_bwd_params* p, mykfa_stream_t stream);
  * delta, then dK/dV, which also stores every 32 x 32 block of dS (rounded to the input type,
  * as the reference rounds it before its dQ product, flash_attn.py:177) into the workspace,
  * then dQ = scale * dS K from those blocks: five products per (query tile, key block) pair
- * instead of seven. Deterministic, no atomics. The workspace holds the dS of whole KV heads:
+ * instead of seven. Deterministic: no sum depends on the order of workgroups (dK/dV takes its
+ * blocks from queues through atomic counters, which decide only which workgroup computes a
+ * block). The workspace holds the dS of whole KV heads and the queue counters:
  * mykfa_bwd_workspace_per_kv_head bytes each (0 when head_dim is not 128, where the trade does
  * not pay); with workspace_bytes >= n times that, KV heads are processed in passes of up to n.
  * With less than one KV head's worth this is mykfa_bwd (dQ recomputes S and dP). */

@@ -63,6 +63,11 @@ struct BwdArgs {
     int64_t ds_hs;
     int ds_w, ds_nqt;
     int kv0;
+    // Block queues of the queued (persistent) stored-dS dK/dV kernel: kQueueSet ints per pass
+    // (one counter per XCD queue) at sched + pass * kQueueSet; the delta kernel zeroes
+    // sched_zero of them. sched == nullptr: grid launch.
+    int* sched;
+    int sched_zero;
 };
 
 typedef __attribute__((address_space(1))) s16x8 gs16x8;
@@ -83,6 +88,143 @@ __device__ inline int ds_tile_base(int b, int64_t tok0, int seqlen_q, bool varle
 // dQ pass touches (keys r..r+3 x both g x both kb) on distinct banks.
 __device__ inline int ds_chunk(int kb, int g, int key) { return 64 * kb + 32 * g + (key ^ (4 * (2 * kb + g))); }
 
+// ---- block queues of the stored-dS dK/dV kernel ------------------------------------------
+//
+// A grid launch over packed sequences is sized by the longest one: most of its workgroups
+// find no work (a rank beyond their sequence) and exit, yet each first waits for a free CU,
+// takes its LDS and loads the sequence bounds. On the 17-document 16K-token batch the
+// dK/dV grid has 5440 workgroups of which 1064 hold work; the others kept the CUs from the
+// long blocks for 11 us at the median and 30 us at worst, and the fixed dispatch order left
+// CUs idle for up to 60 us at the end (timestamps per workgroup). The queued kernel runs one
+// persistent workgroup per CU instead. Each lists, in LDS, the chunks (kXcdChunk consecutive
+// ranks of one (group, sequence) pair, as block_coord numbers them) that hold work, split by
+// the XCD the grid launch places them on; it then takes blocks from its own XCD's queue in
+// that order (longest first) through one atomic counter per queue, and once that queue is
+// empty from the other XCDs' queues. Every block is taken exactly once whatever the
+// placement of the workgroups, and a block's outputs depend on nothing else: the results are
+// bitwise those of the grid launch. (The dS-driven dQ kernel, run the same way, measured 3%
+// slower: its blocks are short and HBM-bound, so the listing and the per-block fetch cost
+// more than the idle CUs of its grid launch.)
+constexpr int kQueueSet = 8;     // counters per pass: one per XCD queue
+constexpr int kQueueCap = 4096;  // chunks a launch may span (LDS list of uint16 entries)
+constexpr size_t kSchedBytes = 4096;  // queue counters' share of each KV head's workspace
+
+struct Queues {
+    uint16_t list[kQueueCap];  // 16 m + span of each listed chunk c = x + kXcds * m
+    int off[kXcds + 1];        // queue x = list[off[x] .. off[x + 1])
+    int wsum[16];
+    int job;
+};
+
+// Lists the chunks c < nchunks that hold work, queue by queue (c % kXcds), each in order, with
+// the ranks within the chunk that hold work: span(c, len) = first | last << 2 (0 <= first <=
+// last < kXcdChunk), or -1 for none, where len is the length of sequence seq_of(c) (any
+// sequence for a padding chunk): cu[seq + 1] - cu[seq], or dense_len without cu. Every read of
+// cu goes out before the first is used (unconditionally, at a valid index), so the listing
+// costs one memory round trip. NT = threads of the workgroup; the caller guarantees
+// nchunks <= kQueueCap.
+template <int NT, typename SeqOf, typename Span>
+__device__ void build_queues(Queues& qs, int nchunks, SeqOf seq_of, const int32_t* cu, int dense_len, Span span) {
+    constexpr int R = (kQueueCap / kXcds + NT - 1) / NT;  // candidates per thread and queue
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    int len[kXcds][R];
+#pragma unroll
+    for (int x = 0; x < kXcds; ++x)
+#pragma unroll
+        for (int r = 0; r < R; ++r) len[x][r] = dense_len;
+    if (cu != nullptr) {
+        int lo[kXcds][R], hi[kXcds][R];
+#pragma unroll
+        for (int x = 0; x < kXcds; ++x)
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int sq = seq_of(x + kXcds * (tid + r * NT));
+                lo[x][r] = cu[sq];
+                hi[x][r] = cu[sq + 1];
+            }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int x = 0; x < kXcds; ++x)
+#pragma unroll
+            for (int r = 0; r < R; ++r) len[x][r] = hi[x][r] - lo[x][r];
+    }
+    int base = 0;
+#pragma unroll
+    for (int x = 0; x < kXcds; ++x) {
+        if (tid == 0) qs.off[x] = base;
+        const int M = nchunks > x ? (nchunks - x + kXcds - 1) / kXcds : 0;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if (r * NT >= M) break;
+            const int m = tid + r * NT;
+            const int f = m < M ? span(x + kXcds * m, len[x][r]) : -1;
+            const bool v = f >= 0;
+            const uint64_t bal = __ballot(v);
+            if (lane == 0) qs.wsum[w] = __popcll(bal);
+            __syncthreads();
+            int before = base, tot = 0;
+            for (int i = 0; i < NT / 64; ++i) {
+                before += i < w ? qs.wsum[i] : 0;
+                tot += qs.wsum[i];
+            }
+            if (v) qs.list[before + __popcll(bal & ((1ull << lane) - 1))] = (uint16_t)(16 * m + f);
+            base += tot;
+            __syncthreads();
+        }
+    }
+    if (tid == 0) qs.off[kXcds] = base;
+    __syncthreads();
+}
+
+// The next block for this workgroup (logical index, as block_coord takes it), or -1 once
+// every queue is empty. q (thread 0's copy) is the queue offset from the workgroup's own XCD
+// it currently draws from; it only moves on. Ranks of a chunk outside its span are passed over
+// without a barrier. Block-uniform call.
+__device__ int next_block(Queues& qs, int* ctr, int xcd, int& q) {
+    if (threadIdx.x == 0) {
+        int job = -1;
+        while (q < kXcds) {
+            const int x = (xcd + q) & (kXcds - 1);
+            const int n = (qs.off[x + 1] - qs.off[x]) * kXcdChunk;
+            const int k = n > 0 ? __hip_atomic_fetch_add(ctr + x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : n;
+            if (k >= n) {
+                ++q;
+                continue;
+            }
+            const int e = qs.list[qs.off[x] + k / kXcdChunk], lo = k % kXcdChunk;
+            if (lo < (e & 3) || lo > ((e >> 2) & 3)) continue;
+            job = (x + kXcds * (e >> 4)) * kXcdChunk + lo;
+            break;
+        }
+        qs.job = job;
+    }
+    __syncthreads();
+    const int job = qs.job;
+    __syncthreads();
+    return job;
+}
+
+// Span code (see build_queues) of the chunk whose ranks start at r0 when ranks [lo, hi) of
+// its pair hold work; -1 for none.
+__device__ inline int rank_span(int r0, int lo, int hi, bool pair_ok) {
+    const int f = lo > r0 ? lo - r0 : 0, l = (hi < r0 + kXcdChunk ? hi : r0 + kXcdChunk) - 1 - r0;
+    return pair_ok && f <= l ? f | l << 2 : -1;
+}
+
+// The kernel's argument block, read afresh by each block of a queued kernel: without the
+// opaque pointer the compiler hoists every argument load out of the block loop and keeps the
+// values in SGPRs across all of a block's work (114 SGPR and 10 VGPR spills in the dK/dV
+// kernel). The argument is the kernel's only one, at offset 0 of the argument segment.
+__device__ inline const BwdArgs& fresh_args() {
+    auto kp = __builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(kp));
+    return *(const BwdArgs*)kp;
+}
+
+__global__ void sched_zero_kernel(int* p, int n) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0;
+}
+
 // ---- 1. delta = rowsum(dO * O) ---------------------------------------------------------
 
 // One flat grid over the (row, head) items: rows run over the packed tokens (varlen:
@@ -99,6 +241,9 @@ __global__ __launch_bounds__(256) void bwd_delta_kernel(BwdArgs a) {
     const int r_lo = varlen ? a.cu_q[0] : 0;
     const int r_hi = varlen ? a.cu_q[a.batch] : a.batch * a.seqlen_q;
     const int64_t n = (int64_t)(r_hi - r_lo) * a.num_heads;
+    // The queue counters of the passes that follow start at zero.
+    if (a.sched != nullptr && blockIdx.x == 0)
+        for (int i = threadIdx.x; i < a.sched_zero; i += 256) a.sched[i] = 0;
     const int ch = threadIdx.x % CPR;
     const int64_t stride = (int64_t)gridDim.x * IPB;
     for (int64_t base = (int64_t)blockIdx.x * IPB + threadIdx.x / CPR; base < n; base += stride * U) {
@@ -560,7 +705,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
 // the barrier that ends its step and a tile has STAGES - 1 steps to land. The HPW partial
 // sums of a key block are added through LDS in a fixed order: no atomics, bitwise repeatable.
 template <int D, int HPW, int STAGES, typename T, bool DS>
-__global__ __launch_bounds__(512) void bwd_dkdv_pair_kernel(BwdArgs a) {
+__device__ __forceinline__ void dkdv_pair_block(const BwdArgs& a, int logical) {
     constexpr int KPW = 4 / HPW;
     constexpr int KD = D / 16;
     constexpr int DB = D / 32;
@@ -579,13 +724,18 @@ __global__ __launch_bounds__(512) void bwd_dkdv_pair_kernel(BwdArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t ring_mem[HPW][STAGES][STAGE];
     __shared__ __attribute__((aligned(16))) float xbuf[2][4][XBUF];
 
-    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    // The thread index through an opaque copy: in the queued kernel's block loop the compiler
+    // would otherwise compute every lane-dependent offset of both roles once before the loop
+    // and hold them all across it (10 VGPR spills); the mask restores the known range.
+    int tid_raw = threadIdx.x;
+    asm volatile("" : "+v"(tid_raw));
+    const int tid = tid_raw & 511, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int l32 = lane & 31, g = lane >> 5;
     const bool role_b = wave >= 4;
     const int pair = wave & 3;
     const int hs = pair / KPW, kbi = pair % KPW;
     // Key blocks are ranked from the END of each sequence (see bwd_dkdv_kernel).
-    const BlockCoord bc = block_coord(xcd_logical(blockIdx.x), a.gz, a.gy, a.cu_k != nullptr);
+    const BlockCoord bc = block_coord(logical, a.gz, a.gy, a.cu_k != nullptr);
     if (bc.rank >= a.gx) return;
     const int kvh = a.kv0 + bc.group;
     const int b = bc.seq;
@@ -936,6 +1086,31 @@ __global__ __launch_bounds__(512) void bwd_dkdv_pair_kernel(BwdArgs a) {
     }
 }
 
+template <int D, int HPW, int STAGES, typename T, bool DS>
+__global__ __launch_bounds__(512) void bwd_dkdv_pair_kernel(BwdArgs a) {
+    dkdv_pair_block<D, HPW, STAGES, T, DS>(a, xcd_logical(blockIdx.x));
+}
+
+// The same blocks from the queues a.sched[0 .. kXcds), one persistent workgroup per CU. A
+// chunk holds work iff its last rank reaches its sequence's first key block (ranks below
+// gx - key blocks of the sequence hold none).
+template <int D, int HPW, int STAGES, typename T>
+__global__ __launch_bounds__(512) void bwd_dkdv_pair_queued_kernel(BwdArgs a) {
+    constexpr int KPW = 4 / HPW;
+    __shared__ Queues qs;
+    const bool varlen = a.cu_k != nullptr;
+    const int P = coord_pairs(a.gz, a.gy, varlen);
+    const int pairs = a.gz * a.gy;
+    build_queues<512>(
+        qs, (a.gx + kXcdChunk - 1) / kXcdChunk * P, [&](int c) { return min(c % P / a.gz, a.gy - 1); },
+        varlen ? a.cu_k : nullptr, a.seqlen_k,
+        [&](int c, int k_len) { return rank_span(c / P * kXcdChunk, a.gx - (k_len + 32 * KPW - 1) / (32 * KPW), a.gx, c % P < pairs); });
+    const int xcd = (int)(__smid() >> 6) & (kXcds - 1);
+    int q = 0;
+    for (int blk = next_block(qs, a.sched, xcd, q); blk >= 0; blk = next_block(qs, a.sched, xcd, q))
+        dkdv_pair_block<D, HPW, STAGES, T, true>(fresh_args(), blk);
+}
+
 // ---- 3. dQ ------------------------------------------------------------------------------
 
 template <int D, int BN, int NW, int STAGES, typename T>
@@ -1152,7 +1327,7 @@ __device__ inline s16x8 lds_tr_block32(const uint16_t* blk, int kb, int lane) {
 // transposed. The pass streams each stored byte once: HBM-bound, except along the longest
 // causal rows, whose chain of steps is covered by the ring's depth.
 template <int D, int NW, int NBK, int STAGES, typename T>
-__global__ __launch_bounds__(NW * 64) void bwd_dq_ds_kernel(BwdArgs a) {
+__device__ __forceinline__ void dq_ds_block(const BwdArgs& a, int logical) {
     constexpr int DB = D / 32;
     constexpr int RQ = 64;
     constexpr int BN = 32 * NBK;
@@ -1168,7 +1343,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_dq_ds_kernel(BwdArgs a) {
     const int l32 = lane & 31, g = lane >> 5;
     const int hpw = a.hpw, kpw = NW / hpw;
     // Longest causal rows first across all heads and sequences, XCD-grouped.
-    const BlockCoord bc = block_coord(xcd_logical(blockIdx.x), a.gz, a.gy, a.cu_q != nullptr);
+    const BlockCoord bc = block_coord(logical, a.gz, a.gy, a.cu_q != nullptr);
     if (bc.rank >= a.gx) return;
     const int b = bc.seq;
     SeqInfo qs = seq_info(b, a.cu_q, nullptr, a.seqlen_q, false);
@@ -1300,6 +1475,11 @@ __global__ __launch_bounds__(NW * 64) void bwd_dq_ds_kernel(BwdArgs a) {
     }
 }
 
+template <int D, int NW, int NBK, int STAGES, typename T>
+__global__ __launch_bounds__(NW * 64) void bwd_dq_ds_kernel(BwdArgs a) {
+    dq_ds_block<D, NW, NBK, STAGES, T>(a, xcd_logical(blockIdx.x));
+}
+
 int gcd_int(int x, int y) {
     while (y) {
         int t = x % y;
@@ -1307,6 +1487,20 @@ int gcd_int(int x, int y) {
         y = t;
     }
     return x;
+}
+
+// Workgroups of a queued launch: per_cu per CU of the current device (a count read once per
+// device). More than can be resident is harmless: every workgroup drains the queues.
+int queued_grid(int per_cu) {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256 * per_cu;
+    if (cus[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev] * per_cu;
 }
 
 BwdArgs make_args(const mykfa_bwd_params& p) {
@@ -1347,6 +1541,8 @@ BwdArgs make_args(const mykfa_bwd_params& p) {
     a.ds_hs = 0;
     a.ds_w = a.ds_nqt = 0;
     a.kv0 = 0;
+    a.sched = nullptr;
+    a.sched_zero = 0;
     return a;
 }
 
@@ -1397,6 +1593,10 @@ hipError_t dkdv_pair_launch_hpw(BwdArgs a, int num_kv_heads, hipStream_t s) {
     const long long n = block_grid_size(a.gx, a.gz, a.gy, a.cu_k != nullptr);
     if (n == 0) return hipSuccess;
     if (n > (1LL << 30)) return hipErrorInvalidConfiguration;
+    if (DS && a.sched != nullptr && n / kXcdChunk <= kQueueCap) {
+        hipLaunchKernelGGL((bwd_dkdv_pair_queued_kernel<D, HPW, STAGES, T>), dim3(queued_grid(1)), dim3(512), 0, s, a);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL((bwd_dkdv_pair_kernel<D, HPW, STAGES, T, DS>), dim3(xcd_grid((int)n)), dim3(512), 0, s, a);
     return hipGetLastError();
 }
@@ -1473,10 +1673,18 @@ hipError_t dq_ds_launch(BwdArgs a, int num_kv_heads, hipStream_t s) {
 // Delta, then per pass of kv_per_pass KV heads: dK/dV storing dS, and dQ from dS.
 template <typename T>
 hipError_t ds_passes(BwdArgs a, const mykfa_bwd_params& p, int kv_per_pass, hipStream_t s) {
+    // Queue counters after the pass's dS (kSchedBytes per KV head of the pass), a set per
+    // pass, zeroed by the delta kernel.
+    const int passes = (p.fwd.num_kv_heads + kv_per_pass - 1) / kv_per_pass;
+    int* const sched = reinterpret_cast<int*>(a.ds + (int64_t)kv_per_pass * a.group * a.ds_hs);
+    const bool queued = (size_t)passes * kQueueSet * sizeof(int) <= (size_t)kv_per_pass * kSchedBytes;
+    a.sched = queued ? sched : nullptr;
+    a.sched_zero = queued ? passes * kQueueSet : 0;
     hipError_t e = preprocess_dtype<T>(a, p.fwd.head_dim, s);
     for (int kv0 = 0; e == hipSuccess && kv0 < p.fwd.num_kv_heads; kv0 += kv_per_pass) {
         const int n = p.fwd.num_kv_heads - kv0 < kv_per_pass ? p.fwd.num_kv_heads - kv0 : kv_per_pass;
         a.kv0 = kv0;
+        a.sched = queued ? sched + (kv0 / kv_per_pass) * kQueueSet : nullptr;
         // dQ: 64 keys per step, 3 stages (144 KB of LDS: one workgroup per CU) measured best
         // among 32 / 64 keys per step and 2-6 stages (the single-workgroup ring holds the most
         // bytes in flight).
@@ -1507,7 +1715,7 @@ size_t bwd_ds_bytes_per_kv_head(const mykfa_bwd_params& p) {
     if (f.head_dim != 128) return 0;
     if (f.batch <= 0 || f.max_seqlen_q <= 0 || f.max_seqlen_k <= 0) return 0;
     const int64_t group = f.num_heads / f.num_kv_heads;
-    return (size_t)(group * ds_tiles(f) * ds_slots(f)) * 2048;
+    return (size_t)(group * ds_tiles(f) * ds_slots(f)) * 2048 + kSchedBytes;
 }
 
 BwdArgs ds_args(const mykfa_bwd_params& p, void* ws) {
@@ -1526,8 +1734,12 @@ hipError_t launch_bwd_ds(const mykfa_bwd_params& p, void* ws, int kv_per_pass, h
 }
 
 hipError_t launch_bwd_ds_half(const mykfa_bwd_params& p, void* ws, bool dq, hipStream_t stream) {
-    const BwdArgs a = ds_args(p, ws);
+    BwdArgs a = ds_args(p, ws);
     const int n = p.fwd.num_kv_heads;
+    // One pass over every KV head: its queue counters after the dS, zeroed here.
+    a.sched = reinterpret_cast<int*>(a.ds + (int64_t)n * a.group * a.ds_hs);
+    hipLaunchKernelGGL(sched_zero_kernel, dim3(1), dim3(64), 0, stream, a.sched, kQueueSet);
+    if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     const bool pair = dkdv_pair_enabled();
     if (p.fwd.dtype == MYKFA_BF16) {
         if (dq) return dq_ds_launch<128, 4, 2, 3, BF16>(a, n, stream);

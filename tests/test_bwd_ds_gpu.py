@@ -220,3 +220,32 @@ def test_halves_are_the_whole():
     torch.cuda.synchronize()
     for x, y in zip(g1, g2):
         assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("docs", [1000, 1100])
+def test_many_documents_either_side_of_the_queue_capacity(docs):
+    """About a thousand packed documents on 4 KV heads (GQA 1, one chunk row): the queued dK/dV
+    kernel lists at most 4096 chunks, so 1000 documents (4004 chunks) run queued and 1100 (4404)
+    take the grid launch. Both give the recomputing backward's dV bit for bit and dK, dQ to
+    bf16 rounding, with no unwritten row."""
+    _say(f"stored-dS backward: {docs} packed documents")
+    lens = torch.randint(1, 200, (docs,), generator=torch.Generator().manual_seed(docs)).tolist()
+    q, k, v, do, out, lse, cu, _ = _problem(lens, lens, 4, 4, 128, torch.bfloat16, False, seed=11)
+    L = _lib.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    wl, wr, sc, mx = fa._UNBOUNDED, 0, 128 ** -0.5, max(lens)
+    fp = fa._fwd_params(q, k, v, out, lse, cu, cu, None, mx, mx, sc, wl, wr)
+    _lib.check(L.mykfa_fwd(ctypes.byref(fp), stream))
+    p_ref, g_ref, _ = _params(q, k, v, out, lse, do, cu, cu, mx, mx, sc, wl, wr)
+    _lib.check(L.mykfa_bwd(ctypes.byref(p_ref), stream))
+    p, grads, _ = _params(q, k, v, out, lse, do, cu, cu, mx, mx, sc, wl, wr)
+    per = L.mykfa_bwd_workspace_per_kv_head(ctypes.byref(p))
+    ws = torch.full((4 * per,), 0xFF, dtype=torch.uint8, device="cuda")
+    _lib.check(L.mykfa_bwd_ws(ctypes.byref(p), ws.data_ptr(), ws.numel(), stream))
+    torch.cuda.synchronize()
+    dq, dk, dv = grads
+    for x in grads:
+        assert not torch.isnan(x).any(), "a block was not computed"
+    assert torch.equal(dv, g_ref[2])
+    torch.testing.assert_close(dk.float(), g_ref[1].float(), rtol=1e-2, atol=1e-2)
+    torch.testing.assert_close(dq.float(), g_ref[0].float(), rtol=2e-2, atol=2e-2)
