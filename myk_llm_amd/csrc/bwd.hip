@@ -704,8 +704,20 @@ __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
 // transposed Q operands in registers for the next step), so a stage is refilled right after
 // the barrier that ends its step and a tile has STAGES - 1 steps to land. The HPW partial
 // sums of a key block are added through LDS in a fixed order: no atomics, bitwise repeatable.
+// Steps it + S .. it + N - 1 of a loop unrolled by N (those below iters), each called with its
+// position S as a compile-time constant.
+template <int S, int N, typename F>
+__device__ __forceinline__ void stage_steps(F& f, int it, int iters) {
+    if constexpr (S < N) {
+        if (it + S < iters) {
+            f(std::integral_constant<int, S>{}, it + S);
+            stage_steps<S + 1, N>(f, it, iters);
+        }
+    }
+}
+
 template <int D, int HPW, int STAGES, typename T, bool DS>
-__device__ __forceinline__ void dkdv_pair_block(const BwdArgs& a, int logical) {
+__device__ __forceinline__ void dkdv_pair_block(const BwdArgs& a, int block) {
     constexpr int KPW = 4 / HPW;
     constexpr int KD = D / 16;
     constexpr int DB = D / 32;
@@ -722,7 +734,7 @@ __device__ __forceinline__ void dkdv_pair_block(const BwdArgs& a, int logical) {
     static_assert(QLOADS % PARTS == 0, "tensor loads split evenly over the issuing waves");
     static_assert(HPW == 1 || 2 * STAGES * STAGE * 2 >= 4 * DB * 16 * 64 * 4, "reduction fits the ring");
     __shared__ __attribute__((aligned(16))) uint16_t ring_mem[HPW][STAGES][STAGE];
-    __shared__ __attribute__((aligned(16))) float xbuf[2][4][XBUF];
+    __shared__ __attribute__((aligned(16))) float xbuf[STAGES][4][XBUF];
 
     // The thread index through an opaque copy: in the queued kernel's block loop the compiler
     // would otherwise compute every lane-dependent offset of both roles once before the loop
@@ -735,7 +747,7 @@ __device__ __forceinline__ void dkdv_pair_block(const BwdArgs& a, int logical) {
     const int pair = wave & 3;
     const int hs = pair / KPW, kbi = pair % KPW;
     // Key blocks are ranked from the END of each sequence (see bwd_dkdv_kernel).
-    const BlockCoord bc = block_coord(logical, a.gz, a.gy, a.cu_k != nullptr);
+    const BlockCoord bc = block_coord(block, a.gz, a.gy, a.cu_k != nullptr);
     if (bc.rank >= a.gx) return;
     const int kvh = a.kv0 + bc.group;
     const int b = bc.seq;
@@ -856,18 +868,21 @@ __device__ __forceinline__ void dkdv_pair_block(const BwdArgs& a, int logical) {
         barrier_lds();
 
         const float qk_scale = sgpr_copy(a.qk_scale);
-        int cur_tile = 0, cur_stage = 0;
-        for (int it = 0; it < iters; ++it) {
+        int cur_tile = 0;
+        // One step per query tile; the ring stage (it % STAGES) is a compile-time constant of
+        // each unrolled step, so every LDS address of the step is a per-lane register plus an
+        // immediate (with a run-time stage the step spent ~40 VALU instructions on addresses).
+        auto a_step = [&](auto SC, int it) {
+            constexpr int stage = decltype(SC)::value;
             // Tile it + STAGES - 1 goes into the stage tile it - 1 used, in three chunks.
             const bool refill = it + STAGES - 1 < iters;
             if (refill) issue_part(C0{}, C1{}, false);
             const int m0 = ur.lo + cur_tile * BMQ;
             const bool masked = !(m0 >= wr.mid_lo && m0 + BMQ <= wr.mid_hi);
-            const uint16_t* Qs = ring + cur_stage * STAGE;
+            const uint16_t* Qs = ring + stage * STAGE;
             const uint16_t* DOs = Qs + TILE;
             const float* fl = reinterpret_cast<const float*>(Qs + 2 * TILE);
             cur_tile = cur_tile + 1 == ntiles ? 0 : cur_tile + 1;
-            cur_stage = cur_stage + 1 == STAGES ? 0 : cur_stage + 1;
             // All operand reads of a product are issued before it (the compiler would otherwise
             // serialize read -> wait -> product): the Q rows and the lse row for S, then the
             // transposed dO operands of dV, whose latency hides under the exponentials.
@@ -898,7 +913,7 @@ __device__ __forceinline__ void dkdv_pair_block(const BwdArgs& a, int logical) {
             // visible from this lane's key iff lo_f <= key - i <= hi_f, i < q_len, key < k_len.
             if (masked) mask_runs16(pv, m0 + 8 * g, key - hi_f, key < k_len ? min(key - lo_f, q_len - 1) : key - hi_f - 1);
             // P for wave B, in chunk-major lane order (16-byte writes, conflict-free).
-            float* xp = &xbuf[it & 1][pair][0];
+            float* xp = &xbuf[stage][pair][0];
 #pragma unroll
             for (int c = 0; c < 4; ++c)
                 *reinterpret_cast<f32x4*>(xp + c * 256 + lane * 4) =
@@ -923,7 +938,8 @@ __device__ __forceinline__ void dkdv_pair_block(const BwdArgs& a, int logical) {
             const int after = iters - 2 - it < STAGES - 2 ? iters - 2 - it : STAGES - 2;
             if (after >= 0) ring_wait<LOADS, STAGES>(after);
             barrier_lds();
-        }
+        };
+        for (int it = 0; it < iters; it += STAGES) stage_steps<0, STAGES>(a_step, it, iters);
     } else {
         // ---- wave B: dP, dS, dK (one tile behind A) ----
         {
@@ -958,8 +974,8 @@ __device__ __forceinline__ void dkdv_pair_block(const BwdArgs& a, int logical) {
         s16x8 qt[DB][2];
         int pm0 = 0;
         uint64_t pds = 0;
-        auto read_p = [&](int pit, f32x4* x) {
-            const float* xp = &xbuf[pit & 1][pair][0];
+        auto read_p = [&](int slot, f32x4* x) {
+            const float* xp = &xbuf[slot][pair][0];
 #pragma unroll
             for (int c = 0; c < 4; ++c) x[c] = *reinterpret_cast<const f32x4*>(xp + c * 256 + lane * 4);
         };
@@ -991,8 +1007,14 @@ __device__ __forceinline__ void dkdv_pair_block(const BwdArgs& a, int logical) {
                     const s16x8 z = {0, 0, 0, 0, 0, 0, 0, 0};
                     // Non-temporal: the dQ pass reads them long after; kept out of the way
                     // of the Q / dO tiles other workgroups reuse through L2 (445 -> 434 us).
-                    __builtin_nontemporal_store(zero_keys ? z : dsb[0], reinterpret_cast<gs16x8*>(blk + ds_lane0));
-                    __builtin_nontemporal_store(zero_keys ? z : dsb[1], reinterpret_cast<gs16x8*>(blk + ds_lane1));
+                    // Keys past the sequence exist only in a sequence's last key block.
+                    s16x8 d0 = dsb[0], d1 = dsb[1];
+                    if (bs < 32) {
+                        d0 = zero_keys ? z : d0;
+                        d1 = zero_keys ? z : d1;
+                    }
+                    __builtin_nontemporal_store(d0, reinterpret_cast<gs16x8*>(blk + ds_lane0));
+                    __builtin_nontemporal_store(d1, reinterpret_cast<gs16x8*>(blk + ds_lane1));
                 }
             }
 #pragma unroll
@@ -1000,16 +1022,18 @@ __device__ __forceinline__ void dkdv_pair_block(const BwdArgs& a, int logical) {
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb) acc[db] = T::mfma32(qt[db][kb], dsb[kb], acc[db]);
         };
-        int cur_tile = 0, cur_stage = 0;
-        for (int it = 0; it < iters; ++it) {
+        int cur_tile = 0;
+        // Unrolled by ring stage like wave A's loop; P of step it sits in xbuf[it % STAGES].
+        auto b_step = [&](auto SC, int it) {
+            constexpr int stage = decltype(SC)::value;
             const int m0 = ur.lo + cur_tile * BMQ;
-            const uint16_t* Qs = ring + cur_stage * STAGE;
+            const uint16_t* Qs = ring + stage * STAGE;
             const uint16_t* DOs = Qs + TILE;
             const float* fl = reinterpret_cast<const float*>(Qs + 2 * TILE);
             // Operand reads first (see wave A): P of the previous tile, this tile's dO rows
             // and delta row.
             f32x4 px[4];
-            if (it > 0) read_p(it - 1, px);
+            if (it > 0) read_p((stage + STAGES - 1) % STAGES, px);
             s16x8 oa[KD];
 #pragma unroll
             for (int kk = 0; kk < KD; ++kk) oa[kk] = lds_row_op<D>(DOs, 0, l32, g, kk);
@@ -1023,7 +1047,6 @@ __device__ __forceinline__ void dkdv_pair_block(const BwdArgs& a, int logical) {
             pds = ds_ptr;
             if (cur_tile + 1 == ntiles) ds_ptr += ds_hstep;
             cur_tile = cur_tile + 1 == ntiles ? 0 : cur_tile + 1;
-            cur_stage = cur_stage + 1 == STAGES ? 0 : cur_stage + 1;
             // Q^T operands of this tile's dK product (kept for the next step), issued after the
             // previous tile's dK products have taken theirs.
 #pragma unroll
@@ -1039,10 +1062,11 @@ __device__ __forceinline__ void dkdv_pair_block(const BwdArgs& a, int logical) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) dpm[r] = dp[r] - dl[r >> 2][r & 3];
             barrier_lds();
-        }
+        };
+        for (int it = 0; it < iters; it += STAGES) stage_steps<0, STAGES>(b_step, it, iters);
         if (iters > 0) {
             f32x4 px[4];
-            read_p(iters - 1, px);
+            read_p((iters - 1) % STAGES, px);
             finish(px);
         }
     }
