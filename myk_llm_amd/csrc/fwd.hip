@@ -206,11 +206,18 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdArgs a) {
         }
         // Online softmax (flash_attn.py:90-96). The row max is taken on the raw scores (c > 0)
         // and the scale is folded into one FMA per score: p = exp2(s c - m).
-        float mx = -INFINITY;
+        // One chain per key block, each step a three-input max (v_max3): 8 NB + NB - 1
+        // instructions for the 16 NB scores instead of 12 NB pairwise ones.
+        float mxb[NB];
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
+        for (int nb = 0; nb < NB; ++nb) {
+            mxb[nb] = fmaxf(st[nb][0], st[nb][1]);
 #pragma unroll
-            for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(st[nb][r], st[nb][r + 1]));
+            for (int r = 2; r < 16; r += 2) mxb[nb] = fmaxf(fmaxf(mxb[nb], st[nb][r]), st[nb][r + 1]);
+        }
+        float mx = mxb[0];
+#pragma unroll
+        for (int nb = 1; nb < NB; ++nb) mx = fmaxf(mx, mxb[nb]);
         mx = max_halves(mx) * c;
         // Lazy rescaling: the running max m moves only when a tile exceeds it by more than
         // kRescaleSlack, so P stays <= 2^kRescaleSlack; O / l and the LSE use the same m, so the
