@@ -138,13 +138,16 @@ class KernelCalls:
             p.dv_batch_stride, p.dv_token_stride, p.dv_head_stride = fa._strides(self.dv)
             self.bp = p
             self.keep.append(dout)
-            # The stored-dS schedule that the autograd backward takes for this shape (head_dim
-            # 128 within the default budget): delta, dK/dV storing dS, dQ from dS.
+            # The schedule that the autograd backward takes for this shape, by the same rule
+            # (fa._plan_ds_workspace): stored dS (delta, dK/dV storing dS, dQ from dS) when at
+            # least one KV head's workspace fits, else the recomputing dQ and dK/dV;
+            # `ds_passes` = the passes of KV heads the stored-dS backward takes (0: recomputing).
             per = self.L.mykfa_bwd_workspace_per_kv_head(ctypes.byref(p))
-            heads = k.shape[-2]
-            self.ws = None
-            if per and heads * per <= fa._ds_budget_bytes():
-                self.ws = torch.empty(heads * per, dtype=torch.uint8, device=q.device)
+            heads, ws = fa._plan_ds_workspace(per, k.shape[-2], fa._ds_budget_bytes(),
+                                              lambda n: torch.empty(n, dtype=torch.uint8, device=q.device),
+                                              lambda: fa._available_bytes(q.device))
+            self.ws = ws
+            self.ds_passes = (k.shape[-2] + heads - 1) // heads if heads > 0 else 0
 
     def fwd(self):
         _lib.check(self.L.mykfa_fwd(ctypes.byref(self.fp), self.stream))
@@ -163,6 +166,9 @@ class KernelCalls:
 
     def dq_ds(self):
         _lib.check(self.L.mykfa_bwd_dq_ws(ctypes.byref(self.bp), self.ws.data_ptr(), self.ws.numel(), self.stream))
+
+    def bwd_ws(self):
+        _lib.check(self.L.mykfa_bwd_ws(ctypes.byref(self.bp), self.ws.data_ptr(), self.ws.numel(), self.stream))
 
 
 class DecodeCalls:
@@ -236,11 +242,15 @@ def measure_prefill(w, steps: int, warmup: int, backward: bool, use_graph: bool 
                      inp["dout"] if backward else None)
     reps = max(steps, 10)
     kern = {"fwd": time_events(kc.fwd, reps)}
-    if backward and kc.ws is not None:
+    if backward and kc.ws is not None and kc.ds_passes == 1:
         # Stored-dS backward: delta, dK/dV (also storing dS), dQ from dS.
         kern["bwd_delta"] = time_events(kc.delta_, reps)
         kern["bwd_dkdv"] = time_events(kc.dkdv_ds, reps)
         kern["bwd_dq"] = time_events(kc.dq_ds, reps)
+    elif backward and kc.ws is not None:
+        # Stored dS over several passes of KV heads (the half entry points need every head's
+        # workspace at once): the whole backward as one entry.
+        kern["bwd_ws_passes"] = time_events(kc.bwd_ws, reps)
     elif backward:
         # Recomputing backward: dQ (which also computes delta = rowsum(dO * O)) then dK/dV.
         kern["bwd_dq"] = time_events(kc.dq_, reps)
@@ -248,7 +258,8 @@ def measure_prefill(w, steps: int, warmup: int, backward: bool, use_graph: bool 
     # Algorithmic FLOPs per launch (convention split: fwd = 2 products; of the 5 backward
     # products, dK/dV's kernel owns S, dP, dV, dK = 2.0 F_fwd and dQ's owns dQ = 0.5 F_fwd;
     # delta is HBM-bound streaming, no credited FLOPs).
-    algo = {"fwd": w.fwd_flops, "bwd_dkdv": 2.0 * w.fwd_flops, "bwd_dq": 0.5 * w.fwd_flops}
+    algo = {"fwd": w.fwd_flops, "bwd_dkdv": 2.0 * w.fwd_flops, "bwd_dq": 0.5 * w.fwd_flops,
+            "bwd_ws_passes": 2.5 * w.fwd_flops}
     del inp, step, kc
     return ms, flops, kern, algo
 
@@ -595,29 +606,37 @@ def measure_syrk(steps: int):
 # --- CPU baseline ---------------------------------------------------------------------------------
 
 
-def cpu_baseline(w, budget_s: float = 12.0):
+def cpu_baseline(w, budget_s: float = 12.0, reps: int = 3):
     """The reference's CPU attention path (fp32 einsum reference(), restated in oracle/) with
-    CPU autograd for the backward, looping per document, on this host's cores; documents are
-    taken in order until budget_s of CPU work has been spent (a bounded sample)."""
+    CPU autograd for the backward, looping per document, on this host's cores. The sample is
+    the leading documents of the workload, taken in order by a first (warm-up) pass until
+    budget_s / (reps + 1) of CPU work has been spent; that sample is then timed `reps` more
+    times and the median repetition is reported (1 warm-up + reps repetitions)."""
     from oracle.attention import reference
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     inp = make_inputs(w, device="cpu", with_grad_out=True)
     cu = inp["cu_seqlens"].tolist()
-    done_pairs, t_total, docs = 0, 0.0, 0
-    for i, (a, b) in enumerate(zip(cu, cu[1:])):
+
+    def run_doc(a, b):
         q, k, v = (inp[n][a:b][None].float().requires_grad_() for n in ("q", "k", "v"))
         do = inp["dout"][a:b][None].float()
         t0 = time.perf_counter()
         out = reference(q, k, v, True, w.window_size)
         torch.autograd.grad(out, (q, k, v), do)
-        t_total += time.perf_counter() - t0
-        n = b - a
-        done_pairs += n * (n + 1) // 2
+        return time.perf_counter() - t0
+
+    # Warm-up pass: fixes the sample.
+    done_pairs, t_warm, docs = 0, 0.0, 0
+    for a, b in zip(cu, cu[1:]):
+        t_warm += run_doc(a, b)
+        done_pairs += (b - a) * (b - a + 1) // 2
         docs += 1
-        if t_total >= budget_s:
+        if t_warm >= budget_s / (reps + 1):
             break
+    times = [sum(run_doc(a, b) for a, b in zip(cu[:docs], cu[1:docs + 1])) for _ in range(reps)]
+    t_total = statistics.median(times)
     flops = 3.5 * 4.0 * done_pairs * w.heads * w.head_dim
     model = ""
     try:
@@ -627,8 +646,10 @@ def cpu_baseline(w, budget_s: float = 12.0):
         pass
     return {"value": round(flops / t_total / 1e12, 6), "unit": "TFLOP/s", "cores": cores, "kind": "port",
             "sample": f"fwd+bwd fp32 oracle (reference() restated, CPU autograd) over the first {docs} of "
-                      f"{len(cu) - 1} {w.name} documents ({done_pairs} visible pairs), {t_total:.1f} s; {model}",
-            "seconds": round(t_total, 3)}
+                      f"{len(cu) - 1} {w.name} documents ({done_pairs} visible pairs); 1 warm-up + {reps} "
+                      f"repetitions, median {t_total:.3f} s (repetitions {', '.join(f'{t:.3f}' for t in times)} s); "
+                      f"{model}",
+            "seconds": round(t_total, 3), "repetitions": reps}
 
 
 # --- HBM traffic from the committed rocprofv3 summary -------------------------------------------------

@@ -68,7 +68,10 @@ typedef struct mykfa_fwd_params {
     int64_t k_batch_stride, k_token_stride, k_head_stride;
     int64_t v_batch_stride, v_token_stride, v_head_stride;
     int64_t o_batch_stride, o_token_stride, o_head_stride;
-    int64_t lse_head_stride; /* = rows */
+    int64_t lse_head_stride; /* = rows: dense batch * max_seqlen_q; packed: at least the packed
+                              * row count cu_seqlens_q[batch] (which only the device holds: a
+                              * smaller stride is not detected, and the stored-dS backward then
+                              * leaves the dQ rows beyond it unwritten) */
     const int32_t* cu_seqlens_q;
     const int32_t* cu_seqlens_k;
     const int32_t* seqused_k;
@@ -374,8 +377,8 @@ int mykfa_decode(const mykfa_decode_params* p, void* workspace, size_t workspace
  * rejected (MYKFA_ERR_WORKSPACE). Every call on one GPU shares that GPU's array: calls that
  * overlap on one GPU (concurrent streams) race and must be serialized by the caller. Nothing
  * in the array needs to start at zero (each call writes every partial its merge reads). The
- * first call on each device resolves the array's address (hipGetSymbolAddress): make one call
- * outside graph capture before capturing. */
+ * first call on each device (the device of `stream`, whichever device is current) resolves the
+ * array's address (hipGetSymbolAddress): make one call outside graph capture before capturing. */
 int mykfa_decode_noalloc(const mykfa_decode_params* p, mykfa_stream_t stream);
 
 /* ---- KV append ------------------------------------------------------------------------ */

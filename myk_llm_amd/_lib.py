@@ -8,6 +8,7 @@ has not been built: there is no fallback implementation.
 from __future__ import annotations
 
 import ctypes
+import struct
 import os
 from pathlib import Path
 
@@ -191,6 +192,41 @@ _STRUCT_SIZES = {
     "mykfa_sizeof_ce_params": CeParams,
     "mykfa_sizeof_syrk_params": SyrkParams,
 }
+
+def _flat_layout(struct_type, base: int = 0, out=None):
+    """(offset, struct code) of every scalar field of a (possibly nested) ctypes struct."""
+    out = [] if out is None else out
+    codes = {_ptr: "Q", _i64: "q", _i32: "i", _f32: "f"}
+    for name, ftype in struct_type._fields_:
+        off = base + getattr(struct_type, name).offset
+        if ftype in codes:
+            out.append((off, codes[ftype]))
+        else:
+            _flat_layout(ftype, off, out)
+    return out
+
+
+def _packer(struct_type) -> struct.Struct:
+    """A struct.Struct that writes every field of struct_type, in declaration order, at its
+    ctypes offset (pad bytes where the C layout has them): filling a parameter block with one
+    pack_into call costs ~1 us where ~30 ctypes attribute stores cost ~8 us, which matters on
+    the eager path of small calls. NULL pointers are passed as 0."""
+    fmt, pos = "<", 0
+    for off, code in _flat_layout(struct_type):
+        if off < pos:
+            raise RuntimeError(f"{struct_type.__name__}: overlapping fields")
+        fmt += "x" * (off - pos) + code
+        pos = off + struct.calcsize("<" + code)
+    fmt += "x" * (ctypes.sizeof(struct_type) - pos)
+    s = struct.Struct(fmt)
+    assert s.size == ctypes.sizeof(struct_type)
+    return s
+
+
+FWD_PACK = _packer(FwdParams)
+BWD_PACK = _packer(BwdParams)
+DECODE_PACK = _packer(DecodeParams)
+
 
 _lib: ctypes.CDLL | None = None
 

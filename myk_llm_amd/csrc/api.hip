@@ -384,6 +384,9 @@ int mykfa_bwd_ws(const mykfa_bwd_params* p, void* workspace, size_t workspace_by
     const size_t per = mykfa::bwd_ds_bytes_per_kv_head(*p);
     if (per == 0 || workspace_bytes < per) return mykfa_bwd(p, stream);
     if (workspace == nullptr) return fail(MYKFA_ERR_INVALID, "workspace is NULL");
+    // dS blocks are written and read as 16-byte chunks and the block-queue counters take
+    // device-scope atomics: the buffer must be 16-byte aligned.
+    if (!aligned16(workspace)) return fail(MYKFA_ERR_INVALID, "mykfa_bwd_ws: workspace must be 16-byte aligned");
     const size_t heads = workspace_bytes / per;
     const int per_pass = heads < (size_t)p->fwd.num_kv_heads ? (int)heads : p->fwd.num_kv_heads;
     return launched(mykfa::launch_bwd_ds(*p, workspace, per_pass, as_stream(stream)), "mykfa_bwd_ws");
@@ -401,6 +404,7 @@ int bwd_ds_half(const mykfa_bwd_params* p, void* workspace, size_t workspace_byt
         return fail(MYKFA_ERR_WORKSPACE, "%s: workspace of %zu bytes, %zu needed (every KV head's dS)", what,
                     workspace_bytes, need);
     if (workspace == nullptr) return fail(MYKFA_ERR_INVALID, "workspace is NULL");
+    if (!aligned16(workspace)) return fail(MYKFA_ERR_INVALID, "%s: workspace must be 16-byte aligned", what);
     return launched(mykfa::launch_bwd_ds_half(*p, workspace, dq, as_stream(stream)), what);
 }
 }  // namespace
@@ -482,7 +486,7 @@ int mykfa_decode_noalloc(const mykfa_decode_params* p, mykfa_stream_t stream) {
     }
     void* ws = nullptr;
     if (splits > 1) {
-        const hipError_t e = mykfa::decode_scratch(&ws);
+        const hipError_t e = mykfa::decode_scratch(as_stream(stream), &ws);
         if (e != hipSuccess)
             return fail(MYKFA_ERR_LAUNCH, "mykfa_decode_noalloc: scratch address: %s", hipGetErrorString(e));
     }

@@ -1,5 +1,7 @@
 // Backward pass (replaces _bwd_dq_kernel and _bwd_dkdv_kernel, flash_attn.py:157-314). No
-// atomics anywhere: results are bitwise deterministic. Two schedules over the same kernels:
+// result is accumulated with atomics: results are bitwise deterministic. (The only atomics are
+// the block-queue counters of the queued stored-dS dK/dV kernel, which decide which workgroup
+// takes a block, never what it computes.) Two schedules over the same kernels:
 //
 // Recomputing (mykfa_bwd; every head_dim): two launches in stream order.
 //   1. dQ: forward-shaped: delta = rowsum(dO * O) for the workgroup's rows first (the

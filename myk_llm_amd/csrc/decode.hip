@@ -552,20 +552,28 @@ hipError_t launch_decode_merge(const mykfa_decode_params& p, int num_splits, con
     return merge_dtype<FP16>(a, p.fwd.head_dim, stream);
 }
 
-hipError_t decode_scratch(void** ptr) {
-    // Device addresses of `scratch`, resolved on the first call made with each device current.
+hipError_t decode_scratch(hipStream_t stream, void** ptr) {
+    // Device addresses of `scratch`, one per GPU, resolved once per device: the device is the
+    // one the launch stream belongs to (not necessarily the current one), made current while its
+    // copy's address is taken.
     constexpr int kMaxDevices = 64;
     static std::mutex mu;
     static void* resolved[kMaxDevices] = {};
     int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
+    hipError_t e = hipStreamGetDevice(stream, &dev);
     if (e != hipSuccess) return e;
     if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
     std::lock_guard<std::mutex> lock(mu);
     if (resolved[dev] == nullptr) {
+        int cur = 0;
+        e = hipGetDevice(&cur);
+        if (e != hipSuccess) return e;
+        if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return e;
         void* p = nullptr;
         e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        const hipError_t back = cur != dev ? hipSetDevice(cur) : hipSuccess;
         if (e != hipSuccess) return e;
+        if (back != hipSuccess) return back;
         if (p == nullptr) return hipErrorInvalidSymbol;
         resolved[dev] = p;
     }

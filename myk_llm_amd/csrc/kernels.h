@@ -30,7 +30,7 @@ hipError_t launch_decode_merge(const mykfa_decode_params& p, int num_splits, con
                                hipStream_t stream);
 // This device's copy of the allocation-free decode's static scratch array (resolved once per
 // device; MYKFA_DECODE_SCRATCH_BYTES long).
-hipError_t decode_scratch(void** ptr);
+hipError_t decode_scratch(hipStream_t stream, void** ptr);
 
 hipError_t launch_kv_append(const mykfa_kv_append_params& p, hipStream_t stream);
 

@@ -53,6 +53,35 @@ def _ds_budget_bytes() -> int:
     return (4 << 30) if mb is None else int(mb) << 20
 
 
+# Requests above this size are also checked against the device's free memory first.
+_DS_CHECK_FREE_ABOVE = 256 << 20
+
+
+def _available_bytes(device: torch.device) -> int:
+    """Device memory a new allocation can take without evicting anything: the driver's free
+    memory plus what torch's caching allocator holds unused."""
+    free, _ = torch.cuda.mem_get_info(device)
+    return free + max(torch.cuda.memory_reserved(device) - torch.cuda.memory_allocated(device), 0)
+
+
+def _plan_ds_workspace(per_head: int, kv_heads: int, budget: int, alloc, available=None):
+    """The stored-dS workspace of the backward: (KV heads per pass, buffer), or (0, None) for
+    the recomputing backward. Takes as many KV heads per pass as the budget allows (at most
+    every head); a request above _DS_CHECK_FREE_ABOVE is first capped at 80 % of
+    `available()` bytes, and an allocation that still fails (torch.OutOfMemoryError) is retried
+    with half as many heads, down to none. Both schedules give results within the same
+    tolerance of the reference, so running out of memory costs speed, never the call."""
+    heads = min(kv_heads, budget // per_head) if per_head > 0 else 0
+    if heads > 0 and available is not None and heads * per_head > _DS_CHECK_FREE_ABOVE:
+        heads = min(heads, int(0.8 * available()) // per_head)
+    while heads > 0:
+        try:
+            return heads, alloc(heads * per_head)
+        except torch.OutOfMemoryError:
+            heads //= 2
+    return 0, None
+
+
 # --- validation (flash_attn.py:331-350) ---------------------------------------------------
 
 
@@ -92,13 +121,18 @@ def _last_dim_contiguous(x: Tensor) -> Tensor:
 
 def _strides(x: Tensor) -> tuple[int, int, int]:
     """(batch, token, head) strides in elements; batch is 0 for packed varlen tensors."""
-    return (x.stride(0), x.stride(1), x.stride(2)) if x.dim() == 4 else (0, x.stride(0), x.stride(1))
+    s = x.stride()
+    return (s[0], s[1], s[2]) if len(s) == 4 else (0, s[0], s[1])
 
 
 def _kernel_ready(x: Tensor) -> Tensor:
     """The kernels read 16 bytes at a time along head_dim: a 16-byte aligned base and
     strides that are multiples of 8 elements. Anything else is copied once."""
-    if x.stride(-1) == 1 and x.data_ptr() % 16 == 0 and all(s % 8 == 0 for s in x.stride()[:-1]):
+    s = x.stride()
+    odd = 0
+    for v in s[:-1]:
+        odd |= v
+    if s[-1] == 1 and not (odd & 7) and not (x.data_ptr() & 15):
         return x
     return x.contiguous()
 
@@ -143,23 +177,33 @@ class _DeviceGuard:
             self.guard.__exit__(*exc)
 
 
-def _fwd_params(q, k, v, out, lse, cu_q, cu_k, seqused_k, max_q, max_k, scale, wl, wr) -> _lib.FwdParams:
+def _fwd_values(q, k, v, out, lse, cu_q, cu_k, seqused_k, max_q, max_k, scale, wl, wr) -> tuple:
+    """The fields of mykfa_fwd_params, in declaration order (NULL pointers as 0)."""
     varlen = cu_q is not None
-    p = _lib.FwdParams()
-    p.q, p.k, p.v, p.o, p.lse = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr()
-    p.q_batch_stride, p.q_token_stride, p.q_head_stride = _strides(q)
-    p.k_batch_stride, p.k_token_stride, p.k_head_stride = _strides(k)
-    p.v_batch_stride, p.v_token_stride, p.v_head_stride = _strides(v)
-    p.o_batch_stride, p.o_token_stride, p.o_head_stride = _strides(out)
-    p.lse_head_stride = lse.stride(0)
-    p.cu_seqlens_q, p.cu_seqlens_k, p.seqused_k = _ptr(cu_q), _ptr(cu_k), _ptr(seqused_k)
-    p.batch = cu_q.numel() - 1 if varlen else q.shape[0]
-    p.num_heads, p.num_kv_heads, p.head_dim = q.shape[-2], k.shape[-2], q.shape[-1]
-    p.max_seqlen_q, p.max_seqlen_k = max_q, max_k
-    p.window_left, p.window_right = wl, wr
-    p.softmax_scale = scale
-    p.dtype = _dtype_code(q.dtype)
-    return p
+    return (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
+            *_strides(q), *_strides(k), *_strides(v), *_strides(out), lse.stride(0),
+            0 if cu_q is None else cu_q.data_ptr(), 0 if cu_k is None else cu_k.data_ptr(),
+            0 if seqused_k is None else seqused_k.data_ptr(),
+            cu_q.numel() - 1 if varlen else q.shape[0], q.shape[-2], k.shape[-2], q.shape[-1],
+            max_q, max_k, wl, wr, scale, _dtype_code(q.dtype))
+
+
+def _bwd_values(fwd_values: tuple, dout, dq, dk, dv, delta) -> tuple:
+    """The fields of mykfa_bwd_params, in declaration order, after those of its fwd member."""
+    return (*fwd_values, dout.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), delta.data_ptr(),
+            *_strides(dout), *_strides(dq), *_strides(dk), *_strides(dv))
+
+
+def _packed(packer, values):
+    """A parameter block (bytes laid out as the C struct) filled in one call."""
+    buf = bytearray(packer.size)
+    packer.pack_into(buf, 0, *values)
+    return buf
+
+
+def _fwd_params(q, k, v, out, lse, cu_q, cu_k, seqused_k, max_q, max_k, scale, wl, wr) -> _lib.FwdParams:
+    return _lib.FwdParams.from_buffer(_packed(_lib.FWD_PACK, _fwd_values(q, k, v, out, lse, cu_q, cu_k, seqused_k,
+                                                                         max_q, max_k, scale, wl, wr)))
 
 
 def _int32(x: Optional[Tensor]) -> Optional[Tensor]:
@@ -175,21 +219,23 @@ def _forward(q: Tensor, k: Tensor, v: Tensor, cu_seqlens_q: Optional[Tensor], cu
              seqused_k: Optional[Tensor], max_seqlen_q: int, max_seqlen_k: int, softmax_scale: float,
              window_left: int, window_right: int) -> tuple[Tensor, Tensor]:
     """O and the base-2 LSE (num_heads, rows), fp32 (flash_attn.py:353-373)."""
-    _same_device(q.device, k=k, v=v, cu_seqlens_q=cu_seqlens_q, cu_seqlens_k=cu_seqlens_k, seqused_k=seqused_k)
+    dev = q.device
+    _same_device(dev, k=k, v=v, cu_seqlens_q=cu_seqlens_q, cu_seqlens_k=cu_seqlens_k, seqused_k=seqused_k)
     varlen = cu_seqlens_q is not None
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
     cu_q, cu_k, seqused = _int32(cu_seqlens_q), _int32(cu_seqlens_k), _int32(seqused_k)
-    rows = q.shape[0] if varlen else q.shape[0] * q.shape[1]
-    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
-    lse = torch.empty((q.shape[-2], rows), dtype=torch.float32, device=q.device)
-    p = _fwd_params(q, k, v, out, lse, cu_q, cu_k, seqused, max_seqlen_q, max_seqlen_k, softmax_scale,
-                    window_left, window_right)
+    shape = q.shape
+    out = torch.empty_like(q, memory_format=torch.contiguous_format)
+    lse = q.new_empty((shape[-2], shape[0] if varlen else shape[0] * shape[1]), dtype=torch.float32)
+    p = _lib.FwdParams.from_buffer(_packed(_lib.FWD_PACK, _fwd_values(
+        q, k, v, out, lse, cu_q, cu_k, seqused, max_seqlen_q, max_seqlen_k, softmax_scale, window_left,
+        window_right)))
     L = _lib.lib()
-    with _DeviceGuard(q.device):
+    with _DeviceGuard(dev):
         if not varlen and 0 < max_seqlen_q <= _DECODE_MAX_Q:
-            _decode_launch(L, p, q.device)
+            _decode_launch(L, p, dev)
         else:
-            _lib.check(L.mykfa_fwd(ctypes.byref(p), _stream(q.device)))
+            _lib.check(L.mykfa_fwd(ctypes.byref(p), _stream(dev)))
     return out, lse
 
 
@@ -232,32 +278,38 @@ def _backward(dout: Tensor, q: Tensor, k: Tensor, v: Tensor, out: Tensor, lse: T
     """dQ, dK, dV (flash_attn.py:376-406)."""
     _same_device(q.device, dout=dout, k=k, v=v, out=out, lse=lse, cu_seqlens_q=cu_seqlens_q,
                  cu_seqlens_k=cu_seqlens_k)
+    return _backward_launch(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+                            softmax_scale, window_left, window_right)
+
+
+def _backward_launch(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+                     softmax_scale, window_left, window_right):
+    """_backward once every tensor is known to be on q's GPU (the autograd node's saved tensors
+    were checked by its forward; the incoming gradient is on the output's device)."""
+    dev = q.device
     dout = _kernel_ready(dout)
     q, k, v, out = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v), _kernel_ready(out)
     cu_q, cu_k = _int32(cu_seqlens_q), _int32(cu_seqlens_k)
-    dq = torch.empty(q.shape, dtype=q.dtype, device=q.device)
-    dk = torch.empty(k.shape, dtype=k.dtype, device=k.device)
-    dv = torch.empty(v.shape, dtype=v.dtype, device=v.device)
+    fmt = torch.contiguous_format
+    dq = torch.empty_like(q, memory_format=fmt)
+    dk = torch.empty_like(k, memory_format=fmt)
+    dv = torch.empty_like(v, memory_format=fmt)
     delta = torch.empty_like(lse)
-    p = _lib.BwdParams()
-    p.fwd = _fwd_params(q, k, v, out, lse, cu_q, cu_k, None, max_seqlen_q, max_seqlen_k, softmax_scale,
-                        window_left, window_right)
-    p.dout, p.dq, p.dk, p.dv, p.delta = dout.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), delta.data_ptr()
-    p.do_batch_stride, p.do_token_stride, p.do_head_stride = _strides(dout)
-    p.dq_batch_stride, p.dq_token_stride, p.dq_head_stride = _strides(dq)
-    p.dk_batch_stride, p.dk_token_stride, p.dk_head_stride = _strides(dk)
-    p.dv_batch_stride, p.dv_token_stride, p.dv_head_stride = _strides(dv)
+    p = _lib.BwdParams.from_buffer(_packed(_lib.BWD_PACK, _bwd_values(_fwd_values(
+        q, k, v, out, lse, cu_q, cu_k, None, max_seqlen_q, max_seqlen_k, softmax_scale, window_left, window_right),
+        dout, dq, dk, dv, delta)))
     L = _lib.lib()
-    with _DeviceGuard(q.device):
+    with _DeviceGuard(dev):
         # dK/dV store dS and dQ is formed from it (five products per block pair instead of
         # seven) when at least one KV head's dS fits the budget; KV heads then go in passes.
         per_head = L.mykfa_bwd_workspace_per_kv_head(ctypes.byref(p))
-        heads = min(k.shape[-2], _ds_budget_bytes() // per_head) if per_head else 0
+        heads, ws = (_plan_ds_workspace(per_head, k.shape[-2], _ds_budget_bytes(),
+                                        lambda n: torch.empty(n, dtype=torch.uint8, device=dev),
+                                        lambda: _available_bytes(dev)) if per_head else (0, None))
         if heads > 0:
-            ws = torch.empty(heads * per_head, dtype=torch.uint8, device=q.device)
-            _lib.check(L.mykfa_bwd_ws(ctypes.byref(p), ws.data_ptr(), ws.numel(), _stream(q.device)))
+            _lib.check(L.mykfa_bwd_ws(ctypes.byref(p), ws.data_ptr(), ws.numel(), _stream(dev)))
         else:
-            _lib.check(L.mykfa_bwd(ctypes.byref(p), _stream(q.device)))
+            _lib.check(L.mykfa_bwd(ctypes.byref(p), _stream(dev)))
     return dq, dk, dv
 
 
@@ -343,32 +395,38 @@ def _fwd(*args):
     return _fwd_op(*args) if _compiling() else _forward(*args)
 
 
-def _bwd(*args):
-    return _bwd_op(*args) if _compiling() else _backward(*args)
-
 
 # --- autograd (flash_attn.py:412-429) ------------------------------------------------------
 
 
 class _FlashAttn(torch.autograd.Function):
+    """The autograd node (flash_attn.py:412-429). With with_lse the LSE is a second,
+    non-differentiable output; without it (the common call) the node has one output, which
+    spares the autograd engine an output edge per call."""
+
     @staticmethod
     def forward(ctx, q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale,
-                window_left, window_right):
+                window_left, window_right, with_lse):
         out, lse = _fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, None, max_seqlen_q, max_seqlen_k, softmax_scale,
                         window_left, window_right)
         ctx.save_for_backward(q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k)
         ctx.args = (max_seqlen_q, max_seqlen_k, softmax_scale, window_left, window_right)
-        ctx.mark_non_differentiable(lse)
-        ctx.set_materialize_grads(False)  # no zero-filled gradient for the lse output
-        return out, lse
+        ctx.set_materialize_grads(False)  # an unused output gets no zero-filled gradient
+        if with_lse:
+            ctx.mark_non_differentiable(lse)
+            return out, lse
+        return out
 
     @staticmethod
-    def backward(ctx, dout, dlse):  # pyright: ignore[reportIncompatibleMethodOverride]
+    def backward(ctx, dout, *_):  # pyright: ignore[reportIncompatibleMethodOverride]
         if dout is None:
-            return (None,) * 10
+            return (None,) * 11
         q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k = ctx.saved_tensors
-        dq, dk, dv = _bwd(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, *ctx.args)
-        return dq, dk, dv, None, None, None, None, None, None, None
+        if _compiling():
+            dq, dk, dv = _bwd_op(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, *ctx.args)
+        else:
+            dq, dk, dv = _backward_launch(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, *ctx.args)
+        return dq, dk, dv, None, None, None, None, None, None, None, None
 
 
 # --- public API (flash_attn.py:442-490) ----------------------------------------------------
@@ -383,8 +441,8 @@ def flash_attn_func(
     _check(q, k, v)
     q, k, v = (_last_dim_contiguous(x) for x in (q, k, v))
     scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(q.shape[-1])
-    out, lse = _FlashAttn.apply(q, k, v, None, None, q.shape[1], k.shape[1], scale, *_window(causal, window_size))
-    return (out, lse) if return_softmax_lse else out
+    wl, wr = _window(causal, window_size)
+    return _FlashAttn.apply(q, k, v, None, None, q.shape[1], k.shape[1], scale, wl, wr, return_softmax_lse)
 
 
 def flash_attn_varlen_func(
@@ -400,9 +458,9 @@ def flash_attn_varlen_func(
     _same_device(q.device, cu_seqlens_q=cu_seqlens_q, cu_seqlens_k=cu_seqlens_k)
     q, k, v = (_last_dim_contiguous(x) for x in (q, k, v))
     scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(q.shape[-1])
-    out, lse = _FlashAttn.apply(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, scale,
-                                *_window(causal, window_size))
-    return (out, lse) if return_softmax_lse else out
+    wl, wr = _window(causal, window_size)
+    return _FlashAttn.apply(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, scale, wl, wr,
+                            return_softmax_lse)
 
 
 def flash_attn_with_kvcache(

@@ -260,3 +260,14 @@ def test_stored_ds_halves_check_their_workspace(L):
         assert fn(ctypes.byref(b), 0x50000, need - 1, None) == _lib.ERR_WORKSPACE
         assert b"needed" in L.mykfa_last_error()
         assert fn(ctypes.byref(_bwd_params(64)), 0x50000, 1 << 30, None) == _lib.ERR_UNSUPPORTED
+
+
+def test_stored_ds_entry_points_need_an_aligned_workspace(L):
+    """dS blocks move as 16-byte chunks and the block-queue counters take device-scope atomics:
+    mykfa_bwd_ws and both halves refuse a workspace that is not 16-byte aligned, on the host,
+    before any launch."""
+    b = _bwd_params(128)
+    need = 2 * L.mykfa_bwd_workspace_per_kv_head(ctypes.byref(b))
+    for fn in (L.mykfa_bwd_ws, L.mykfa_bwd_dkdv_ws, L.mykfa_bwd_dq_ws):
+        assert fn(ctypes.byref(b), 0x50008, need, None) == _lib.ERR_INVALID
+        assert b"aligned" in L.mykfa_last_error()

@@ -113,3 +113,45 @@ def test_device_and_dtype_guards_raise_on_the_host():
         _check_append(cache, cache, new.half(), new.half(), torch.zeros(1, dtype=torch.int32))
     with pytest.raises(TypeError):
         _check_append(cache, cache, new.float(), new, torch.zeros(1, dtype=torch.int32))
+
+
+def test_ds_workspace_plan_caps_and_falls_back():
+    """The backward's stored-dS workspace: as many KV heads per pass as the budget allows,
+    capped by the device's available memory above a size threshold, halved on an allocation
+    failure, and none (the recomputing backward) when even one head cannot be allocated."""
+    import torch
+
+    from myk_llm_amd.flash_attn import _DS_CHECK_FREE_ABOVE, _plan_ds_workspace
+
+    got = []
+
+    def alloc(n):
+        got.append(n)
+        return n
+
+    per = 300 << 20
+    assert _plan_ds_workspace(per, 4, 4 << 30, alloc) == (4, 4 * per)
+    assert _plan_ds_workspace(per, 4, 2 * per + 5, alloc) == (2, 2 * per)
+    assert _plan_ds_workspace(0, 4, 4 << 30, alloc) == (0, None)
+    assert _plan_ds_workspace(per, 4, per - 1, alloc) == (0, None)
+    # Available memory caps a large request at 80 %.
+    assert _plan_ds_workspace(per, 4, 4 << 30, alloc, lambda: 3 * per)[0] == 2
+    # Small requests skip the query.
+    small = _DS_CHECK_FREE_ABOVE // 4
+    assert _plan_ds_workspace(small, 4, 4 << 30, alloc, lambda: 0)[0] == 4
+
+    calls = []
+
+    def oom_above(limit):
+        def f(n):
+            calls.append(n)
+            if n > limit:
+                raise torch.OutOfMemoryError("planted")
+            return n
+        return f
+
+    assert _plan_ds_workspace(per, 4, 4 << 30, oom_above(per)) == (1, per)
+    assert calls == [4 * per, 2 * per, per]
+    calls.clear()
+    assert _plan_ds_workspace(per, 4, 4 << 30, oom_above(0)) == (0, None)
+    assert calls == [4 * per, 2 * per, per]
