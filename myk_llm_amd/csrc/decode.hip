@@ -7,10 +7,17 @@
 // is read from HBM once per GQA group, not once per query head. With GROUP = 4 and the
 // 4-query MTP draft this exactly fills the tile.
 //
-// Split-K. Workgroup (split, batch, unit block) covers the keys [split * chunk, (split + 1) *
-// chunk) of its sequence for kWaves consecutive (KV head, row tile) units, one per wave, so the
-// waves of a workgroup read adjacent heads of the same cache rows (contiguous DRAM rows in the
-// usual (batch, token, head, d) layout) and share nothing: no barrier, no cross-wave merge.
+// Split-K, balanced by length. A split-K pass takes as long as its most loaded CU: with splits
+// sized from the cache capacity (the host knows no lengths) a batch of random lengths left
+// half the workgroups empty and some CUs with two full splits (measured on 64 sequences of
+// U[256, 16384] keys: 74-107 us for the same bytes depending only on where split boundaries
+// fell). So every workgroup first reads the sequences' lengths and computes the same plan on
+// the device: a chunk target T from the total visible keys such that the active workgroups fit
+// one resident round, s_b = ceil(V_b / T) equal splits for sequence b, numbered sequence by
+// sequence; workgroup x takes split x of that numbering (assign_split). Each covers its split's
+// keys for kWaves consecutive (KV head, row tile) units, one per wave, so the waves of a
+// workgroup read adjacent heads of the same cache rows (contiguous DRAM rows in the usual
+// (batch, token, head, d) layout) and share nothing after the plan: no cross-wave merge.
 // A wave streams its keys in 32-key tiles through a ring of NBUF register tiles filled by
 // bounds-checked buffer loads (NBUF - 1 tiles in flight while one computes). Every load reads
 // whole 128-byte lines (8 lanes per key row of 64 elements): a load in the MFMA operand layout
@@ -18,8 +25,8 @@
 // same bytes. The tile then goes through wave-private LDS: K is read back as the A operand of
 // S^T = K Q^T on 16x16x32 MFMA, then the online softmax, and V is read back transposed for
 // O^T += V^T P^T. A wave then
-// writes either the final O/LSE (one split) or an fp32 partial (O, lse) that the merge kernel
-// combines: lse = log2(sum_s 2^lse_s), O = sum_s 2^(lse_s - lse) O_s.
+// writes either the final O/LSE (a sequence of one split) or an fp32 partial (O, lse) that the
+// merge kernel combines: lse = log2(sum_s 2^lse_s), O = sum_s 2^(lse_s - lse) O_s.
 #include <mutex>
 
 #include "common.h"
@@ -57,14 +64,18 @@ struct DecodeArgs {
     int row_tiles; // ceil(rows / 16)
     int units;     // num_kv_heads * row_tiles (one wave each)
     int num_heads;
-    int chunk;     // keys per split (multiple of kTile)
-    int splits;
+    int nseg;      // partial segments the workspace holds: slots per sequence * batch
+    int resident;  // workgroups the chip holds at once (the balance target)
     int n_new;     // keys appended after seqused_k[b] in this step
     const uint16_t* kn;  // new keys / values to write into the caches first, or null
     const uint16_t* vn;
     int64_t knbs, knts, knhs, vnbs, vnts, vnhs;
-    float* ws_o;   // [batch][num_heads][nq][splits][D]: a row's partials are contiguous
-    float* ws_lse; // [batch][num_heads][nq][splits]
+    // Partials of segment = (first segment of the sequence) + split. A partial O is the
+    // normalized output of its split, a convex combination of V rows, so it is stored in the
+    // 16-bit input type (it cannot leave V's range); the lse stays fp32.
+    uint16_t* ws_o;  // [nseg][num_heads][nq][D]
+    float* ws_lse;   // [nseg][num_heads][nq]
+    int* seg_hdr;  // [batch][2]: first segment and split count of each sequence, for the merge
     int batch;
 };
 
@@ -88,6 +99,127 @@ __device__ inline Ranges decode_ranges(const DecodeArgs& a, int L) {
 template <int D>
 constexpr int decode_nbuf() { return D <= 64 ? 3 : 2; }  // measured at D = 64: 3 > 4 > 6 tiles
 
+// Visible keys of sequence b: the kTile-aligned range any of its rows can see.
+__device__ inline int visible_keys(const DecodeArgs& a, int b) {
+    const Ranges rg = decode_ranges(a, seq_keys(a, b));
+    return rg.hi > rg.lo ? rg.hi - rg.lo : 0;
+}
+
+// Keys per split of the length-balanced split-K (a multiple of kTile) for K visible keys in
+// all: the launch's active workgroups should fit one resident round of the chip (a.resident
+// workgroup slots), since a split-K pass takes as long as its most loaded CU. Sequence b then
+// takes s_b = max(1, ceil(V_b / T)) splits of ceil(V_b / s_b) keys; with A the target count,
+// sum s_b <= K / T + batch <= A + batch <= a.nseg, so the segments always fit the workspace.
+__device__ inline int balanced_chunk(const DecodeArgs& a, long long K) {
+    if (a.nseg <= a.batch) return 1 << 30;  // one slot per sequence: one split each
+    long long A = (long long)min(a.resident, a.nseg) - a.batch;
+    if (A < 1) A = a.nseg - a.batch;
+    long long T = (K + A - 1) / A;
+    T = (T + kTile - 1) / kTile * kTile;
+    return (int)(T < kTile ? kTile : (T > (1 << 30) ? (1 << 30) : T));
+}
+
+// Splits of a sequence with V visible keys under chunk target T.
+__device__ inline int seq_splits(int V, int T) { return V > T ? (V + T - 1) / T : 1; }
+
+struct SplitOf {
+    int b;      // sequence, or -1 when the workgroup holds no split
+    int split;  // index of the split within the sequence
+    int n;      // splits of the sequence
+    int seg;    // workspace segment of split 0 (segments of a sequence are consecutive)
+    int chunk;  // keys per split of the sequence (a multiple of kTile)
+};
+
+// Workgroup w's split of the length-balanced split-K: the sequences' visible key counts V_b
+// are read on the device (every workgroup computes the same plan), T follows from their sum
+// (balanced_chunk), and the splits are numbered sequence by sequence, so workgroup w takes the
+// split whose running index is w; workgroups beyond the last split exit. The first batch
+// workgroups (of z-slice 0) also record (first segment, splits) of sequence w for the merge.
+// Block-uniform call: every thread of the workgroup takes part (two passes over the batch,
+// NT sequences at a time, with block-wide reductions through `red`).
+template <int NT>
+__device__ SplitOf assign_split(const DecodeArgs& a, int w, bool write_header, int* red) {
+    constexpr int NW = NT / 64;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    // Pass 1: K = sum of V_b. One register holds V_b when the batch fits one pass.
+    int v_keep = 0;
+    long long kpart = 0;
+    for (int b0 = 0; b0 < a.batch; b0 += NT) {
+        const int b = b0 + tid;
+        const int v = b < a.batch ? visible_keys(a, b) : 0;
+        if (b0 == 0) v_keep = v;
+        kpart += v;
+    }
+    long long* redll = reinterpret_cast<long long*>(red);
+    auto block_sum = [&](long long x) {
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
+        if (lane == 0) redll[wv] = x;
+        __syncthreads();
+        long long t = 0;
+#pragma unroll
+        for (int i = 0; i < NW; ++i) t += redll[i];
+        __syncthreads();
+        return t;
+    };
+    // (Filling the slots more closely, with a smaller target that a count of the actual
+    // splits allows, measured slower: 501 active workgroups took 83.2 us where 476 took 81.2.)
+    const int T = balanced_chunk(a, block_sum(kpart));
+    // Pass 2: exclusive scan of s_b; the thread whose sequence holds split w records it.
+    SplitOf r = {-1, 0, 0, 0, 0};
+    int* slot = red + 2 * NW;  // [0..4]: the found split
+    if (tid == 0) slot[0] = -1;
+    int run = 0;
+    for (int b0 = 0; b0 < a.batch; b0 += NT) {
+        const int b = b0 + tid;
+        const int v = b < a.batch ? (b0 == 0 ? v_keep : visible_keys(a, b)) : 0;
+        const int s = b < a.batch ? seq_splits(v, T) : 0;
+        int inc = s;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int y = __shfl_up(inc, off);
+            if (lane >= off) inc += y;
+        }
+        if (lane == 63) red[wv] = inc;
+        __syncthreads();
+        int before = run, tot = 0;
+#pragma unroll
+        for (int i = 0; i < NW; ++i) {
+            before += i < wv ? red[i] : 0;
+            tot += red[i];
+        }
+        const int seg0 = before + inc - s;
+        if (b < a.batch) {
+            if (w >= seg0 && w < seg0 + s) {
+                const int c = (v + s - 1) / s;
+                slot[0] = b;
+                slot[1] = w - seg0;
+                slot[2] = s;
+                slot[3] = seg0;
+                int ck = c < kTile ? kTile : (c + kTile - 1) / kTile * kTile;
+                // Splits start ck cache rows apart; power-of-two distances put concurrently
+                // starting workgroups on the same DRAM channels (measured ~15% slower).
+                if (ck > kTile && (ck & (ck - 1)) == 0) ck += kTile;
+                slot[4] = ck;
+            }
+            if (write_header && b == w) {
+                a.seg_hdr[2 * b] = seg0;
+                a.seg_hdr[2 * b + 1] = s;
+            }
+        }
+        run += tot;
+        __syncthreads();
+    }
+    r.b = slot[0];
+    if (r.b >= 0) {
+        r.split = slot[1];
+        r.n = slot[2];
+        r.seg = slot[3];
+        r.chunk = slot[4];
+    }
+    return r;
+}
+
 template <int D, typename T>
 __global__ __launch_bounds__(kThreads) void decode_splitk_kernel(DecodeArgs a) {
     constexpr int KD = D < 32 ? 1 : D / 32;  // 32-wide d steps of S^T (D = 16 pads to 32)
@@ -104,26 +236,32 @@ __global__ __launch_bounds__(kThreads) void decode_splitk_kernel(DecodeArgs a) {
     const int tid = __builtin_amdgcn_workitem_id_x();
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int l16 = lane & 15, G = lane >> 4;
-    const int split = blockIdx.x, b = blockIdx.y;
-    // Wave = one (KV head, row tile) unit; the waves of a workgroup take consecutive units,
-    // i.e. adjacent heads of the same cache rows. No state is shared between waves.
+    // Workgroup (x, 0, z) = split x of the launch's running split index (assign_split) for
+    // kWaves consecutive (KV head, row tile) units z * kWaves ..; one unit per wave: the waves of
+    // a workgroup read adjacent heads of the same cache rows and share nothing after the plan.
+    __shared__ int plan_red[2 * kWaves + 5];
+    const SplitOf so = assign_split<kThreads>(a, blockIdx.x, blockIdx.z == 0 && a.seg_hdr != nullptr, plan_red);
+    if (so.b < 0) return;
+    const int split = so.split, b = so.b;
     const int unit = blockIdx.z * kWaves + wave;
     if (unit >= a.units) return;
     const int kvh = unit / a.row_tiles, rt = unit % a.row_tiles;
 
     const int L = seq_keys(a, b);
+    const Ranges rg = decode_ranges(a, L);
     if (a.kn) {
         // This step's new keys first (flash_attn.py:480-485): the wave writes the rows of its KV
-        // head that fall in its split's key range, whatever their visibility, and drops rows at
-        // or beyond the capacity. Every wave reading a row wrote it itself (waves of further row
-        // tiles of a head write identical copies), and the wait below orders its stores before
-        // its loads.
+        // head that fall in its split's key range (rows before the visible range go to split 0),
+        // whatever their visibility, and drops rows at or beyond the capacity. Every wave
+        // reading a row wrote it itself (waves of further row tiles of a head write identical
+        // copies), and the wait below orders its stores before its loads.
         const int base = a.seqused_k[b];
         constexpr int CPR = D / 8;
         for (int i = lane; i < a.n_new * CPR; i += 64) {
             const int t = i / CPR, ch = i % CPR;
             const int pos = base + t;
-            if (pos < 0 || pos >= a.cap || pos / a.chunk != split) continue;
+            const int owner = pos < rg.lo ? 0 : min((pos - rg.lo) / so.chunk, so.n - 1);
+            if (pos < 0 || pos >= a.cap || owner != split) continue;
             const int64_t src_k = (int64_t)b * a.knbs + (int64_t)t * a.knts + (int64_t)kvh * a.knhs + ch * 8;
             const int64_t src_v = (int64_t)b * a.vnbs + (int64_t)t * a.vnts + (int64_t)kvh * a.vnhs + ch * 8;
             const int64_t dst_k = (int64_t)b * a.kbs + (int64_t)pos * a.kts + (int64_t)kvh * a.khs + ch * 8;
@@ -132,11 +270,8 @@ __global__ __launch_bounds__(kThreads) void decode_splitk_kernel(DecodeArgs a) {
             st16(const_cast<uint16_t*>(a.v) + dst_v, ld16(a.vn + src_v));
         }
     }
-    const Ranges rg = decode_ranges(a, L);
-    int k0 = split * a.chunk, k1 = k0 + a.chunk;
-    k0 = k0 > rg.lo ? k0 : rg.lo;
-    k1 = k1 < rg.hi ? k1 : rg.hi;
-    if (a.splits > 1 && k0 >= k1) return;  // this split holds no visible key: the merge skips it
+    const int k0 = rg.lo + split * so.chunk;
+    const int k1 = k0 + so.chunk < rg.hi ? k0 + so.chunk : rg.hi;  // k1 <= k0 only for an empty sequence
     const int lo_off = band_lo(L, a.nq, a.wl), hi_off = band_hi(L, a.nq, a.wr);
 
     // Q^T operand: lane holds Q[row l16][32 kk + 8 G + i].
@@ -304,7 +439,7 @@ __global__ __launch_bounds__(kThreads) void decode_splitk_kernel(DecodeArgs a) {
     if (!row_ok) return;
     const bool empty = l_row == 0.f;
     const float inv = empty ? 0.f : 1.f / l_row;
-    if (a.splits == 1) {
+    if (so.n == 1) {
         // Final output (flash_attn.py:147-154): lane writes d = 16 db + 4 G .. + 3 of its row.
         uint16_t* op = a.o + (int64_t)b * a.obs + (int64_t)qi * a.ots + (int64_t)h * a.ohs;
 #pragma unroll
@@ -317,44 +452,50 @@ __global__ __launch_bounds__(kThreads) void decode_splitk_kernel(DecodeArgs a) {
         }
         if (G == 0) a.lse[(int64_t)h * a.lse_hs + (int64_t)b * a.nq + qi] = empty ? INFINITY : m_i + fast_log2(l_row);
     } else {
-        // Normalized partial: O_s = o / l, lse_s = m + log2(l) (-inf when empty).
-        const int64_t prow = ((((int64_t)b * a.num_heads + h) * a.nq + qi) * a.splits) + split;
+        // Normalized partial: O_s = o / l (16-bit), lse_s = m + log2(l) (-inf when empty).
+        const int64_t prow = ((int64_t)(so.seg + split) * a.num_heads + h) * a.nq + qi;
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
             const int d0 = 16 * db + 4 * G;
-            if (d0 < D) *reinterpret_cast<f32x4*>(a.ws_o + prow * D + d0) = acc[db] * inv;
+            if (d0 < D) {
+                u32x2 w = {T::pack2(acc[db][0] * inv, acc[db][1] * inv), T::pack2(acc[db][2] * inv, acc[db][3] * inv)};
+                *reinterpret_cast<u32x2*>(a.ws_o + prow * D + d0) = w;
+            }
         }
         if (G == 0) a.ws_lse[prow] = empty ? -INFINITY : m_i + fast_log2(l_row);
     }
 }
 
-// Merge of one output row (batch, head, query) from the n split partials [s_lo, s_lo + n):
-// lse = log2(sum_s 2^lse_s), O = sum_s 2^(lse_s - lse) O_s. The splits go in chunks of up to
-// 64 (lane = split for the lse values; LPS lanes per partial O row, float4 each), and every
-// load of a chunk is issued before the first is used, so a row costs one memory round trip
-// per chunk; chunks after the first rescale the running sums to the new maximum.
+// Merge of one output row (batch, head, query) from the n split partials of its sequence,
+// segments seg0 .. seg0 + n - 1: lse = log2(sum_s 2^lse_s), O = sum_s 2^(lse_s - lse) O_s.
+// The splits go in chunks of up to 64 (lane = split for the lse values; LPS lanes per partial O
+// row, 8 elements each), and every load of a chunk is issued before the first is used, so a
+// row costs one memory round trip per chunk; chunks after the first rescale the running sums to
+// the new maximum.
 template <int D, typename T>
-__device__ inline void merge_row(const DecodeArgs& a, int64_t rowid, int b, int hh, int qq, int s_lo, int n, int lane) {
-    constexpr int LPS = D / 4;                          // lanes per split row (float4 each)
+__device__ inline void merge_row(const DecodeArgs& a, int b, int hh, int qq, int seg0, int n, int lane) {
+    constexpr int LPS = D / 8;                          // lanes per split row (16 bytes each)
     constexpr int SPI = 64 / LPS;                       // split rows per wave-wide load
     constexpr int CH = SPI * 16 < 64 ? SPI * 16 : 64;   // splits per chunk (<= 16 loads per lane)
     constexpr int NL = CH / SPI;
-    const __amdgpu_buffer_rsrc_t lrs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float*>(a.ws_lse + rowid * a.splits + s_lo), (short)0, n * 4, 0x00020000);
-    const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float*>(a.ws_o + (rowid * a.splits + s_lo) * D), (short)0, n * D * 4, 0x00020000);
-    const int sub = lane / LPS, d0 = (lane % LPS) * 4;
+    const int64_t rs = (int64_t)a.num_heads * a.nq;     // lse values between consecutive segments
+    const int64_t row0 = ((int64_t)seg0 * a.num_heads + hh) * a.nq + qq;
+    const float* lp = a.ws_lse + row0;
+    const uint16_t* op = a.ws_o + row0 * D;
+    const int sub = lane / LPS, d0 = (lane % LPS) * 8;
     float M = -INFINITY, lsum = 0.f;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int c0 = 0; c0 < n; c0 += CH) {
         const int cnt = n - c0 < CH ? n - c0 : CH;
-        float ls = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(lrs, (c0 + lane) * 4, 0, 0));
-        f32x4 ov[NL];
+        float ls = -INFINITY;
+        if (lane < cnt) ls = lp[(int64_t)(c0 + lane) * rs];
+        s16x8 ov[NL];
 #pragma unroll
-        for (int u = 0; u < NL; ++u)
-            ov[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                ors, ((c0 + u * SPI + sub) * D + d0) * 4, 0, 0));
-        ls = lane < cnt ? ls : -INFINITY;
+        for (int u = 0; u < NL; ++u) {
+            const int sp = c0 + u * SPI + sub;
+            ov[u] = s16x8{0, 0, 0, 0, 0, 0, 0, 0};
+            if (sp < n) ov[u] = ld16(op + (int64_t)sp * rs * D + d0);
+        }
         float mc = ls;
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) mc = fmaxf(mc, __shfl_xor(mc, off));
@@ -366,26 +507,32 @@ __device__ inline void merge_row(const DecodeArgs& a, int64_t rowid, int b, int 
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) ws += __shfl_xor(ws, off);
         lsum = lsum * sc + ws;
-        acc *= sc;
 #pragma unroll
-        for (int u = 0; u < NL; ++u) acc += __shfl(w, u * SPI + sub) * ov[u];
+        for (int c = 0; c < 8; ++c) acc[c] *= sc;
+#pragma unroll
+        for (int u = 0; u < NL; ++u) {
+            const float wu = __shfl(w, u * SPI + sub);
+#pragma unroll
+            for (int c = 0; c < 8; ++c) acc[c] += wu * T::to_float((uint16_t)ov[u][c]);
+        }
         M = m_new;
     }
 #pragma unroll
     for (int off = LPS; off < 64; off <<= 1)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) acc[c] += __shfl_xor(acc[c], off);
+        for (int c = 0; c < 8; ++c) acc[c] += __shfl_xor(acc[c], off);
     const bool empty = M == -INFINITY;
     const float inv = empty ? 0.f : 1.f / lsum;
     if (lane < LPS) {
-        uint16_t* out = a.o + (int64_t)b * a.obs + (int64_t)qq * a.ots + (int64_t)hh * a.ohs + lane * 4;
-        u32x2 wv = {T::pack2(acc[0] * inv, acc[1] * inv), T::pack2(acc[2] * inv, acc[3] * inv)};
-        *reinterpret_cast<u32x2*>(out) = wv;
+        uint16_t* out = a.o + (int64_t)b * a.obs + (int64_t)qq * a.ots + (int64_t)hh * a.ohs + lane * 8;
+        u32x4 wv = {T::pack2(acc[0] * inv, acc[1] * inv), T::pack2(acc[2] * inv, acc[3] * inv),
+                    T::pack2(acc[4] * inv, acc[5] * inv), T::pack2(acc[6] * inv, acc[7] * inv)};
+        *reinterpret_cast<u32x4*>(out) = wv;
     }
     if (lane == 0) a.lse[(int64_t)hh * a.lse_hs + (int64_t)b * a.nq + qq] = empty ? INFINITY : M + fast_log2(lsum);
 }
 
-// One wave per output row.
+// One wave per output row; rows of a sequence of one split were written by the split-K pass.
 template <int D, typename T>
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -395,12 +542,25 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
     const int qq = rowid % a.nq;
     const int hh = (rowid / a.nq) % a.num_heads;
     const int b = rowid / ((int64_t)a.nq * a.num_heads);
-    const int L = seq_keys(a, b);
-    const Ranges rg = decode_ranges(a, L);
-    const int s_lo = rg.lo / a.chunk;
-    int s_hi = rg.hi > rg.lo ? (rg.hi - 1) / a.chunk + 1 : s_lo;
-    if (s_hi > a.splits) s_hi = a.splits;
-    merge_row<D, T>(a, rowid, b, hh, qq, s_lo, s_hi - s_lo, lane);
+    const int seg0 = a.seg_hdr[2 * b], n = a.seg_hdr[2 * b + 1];
+    if (n <= 1) return;
+    merge_row<D, T>(a, b, hh, qq, seg0, n, lane);
+}
+
+// Split-K workgroups the current device holds at once: two per CU (64 KB of LDS each) up to
+// head_dim 128, one at 256. The CU count is read once per device.
+int resident_slots(int head_dim) {
+    static int cus[64] = {};
+    int dev = 0, n = 256;
+    if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
+        if (cus[dev] == 0) {
+            int c = 0;
+            if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+            cus[dev] = c;
+        }
+        n = cus[dev];
+    }
+    return n * (head_dim > 128 ? 1 : 2);
 }
 
 DecodeArgs make_args(const mykfa_decode_params& p, int splits, void* ws) {
@@ -433,24 +593,21 @@ DecodeArgs make_args(const mykfa_decode_params& p, int splits, void* ws) {
     a.row_tiles = (a.rows + 15) / 16;
     a.units = f.num_kv_heads * a.row_tiles;
     a.num_heads = f.num_heads;
-    a.splits = splits;
-    int chunk = (f.max_seqlen_k + splits - 1) / splits;
-    chunk = (chunk + kTile - 1) / kTile * kTile;
-    chunk = chunk > 0 ? chunk : kTile;
-    // Splits start chunk cache rows apart; power-of-two distances put the concurrently
-    // starting workgroups on the same DRAM channels (measured ~15% slower), so step off them.
-    if (chunk > kTile && (chunk & (chunk - 1)) == 0) chunk += kTile;
-    a.chunk = chunk;
     a.batch = f.batch;
-    const size_t rows_total = (size_t)f.batch * f.num_heads * f.max_seqlen_q;
-    a.ws_o = static_cast<float*>(ws);
-    a.ws_lse = ws ? a.ws_o + (size_t)splits * rows_total * f.head_dim : nullptr;
+    a.nseg = splits > 1 ? splits * f.batch : f.batch;
+    a.resident = resident_slots(f.head_dim) / ((a.units + kWaves - 1) / kWaves);
+    const size_t seg_rows = (size_t)f.num_heads * f.max_seqlen_q;
+    a.ws_o = splits > 1 ? static_cast<uint16_t*>(ws) : nullptr;
+    a.ws_lse = splits > 1 ? reinterpret_cast<float*>(a.ws_o + (size_t)a.nseg * seg_rows * f.head_dim) : nullptr;
+    a.seg_hdr = splits > 1 ? reinterpret_cast<int*>(a.ws_lse + (size_t)a.nseg * seg_rows) : nullptr;
     return a;
 }
 
 template <typename T>
 hipError_t splitk_dtype(const DecodeArgs& a, int D, int num_kv_heads, hipStream_t s) {
-    dim3 grid(a.splits, a.batch, (a.units + kWaves - 1) / kWaves);
+    // Split slots: every sequence's splits are numbered in one running index (assign_split);
+    // slots past the last split exit at once (they are dispatched last).
+    dim3 grid(a.nseg, 1, (a.units + kWaves - 1) / kWaves);
     switch (D) {
         case 16: hipLaunchKernelGGL((decode_splitk_kernel<16, T>), grid, dim3(kThreads), 0, s, a); break;
         case 32: hipLaunchKernelGGL((decode_splitk_kernel<32, T>), grid, dim3(kThreads), 0, s, a); break;
@@ -509,7 +666,9 @@ __global__ __launch_bounds__(256) void kv_append_kernel(mykfa_kv_append_params p
 size_t decode_workspace_bytes(int batch, int num_heads, int seqlen_q, int head_dim, int num_splits) {
     if (num_splits <= 1) return 0;
     const size_t rows = (size_t)batch * num_heads * seqlen_q;
-    return (size_t)num_splits * rows * ((size_t)head_dim + 1) * sizeof(float);
+    // Partial O and lse of num_splits segments per sequence on average, then the per-sequence
+    // (first segment, split count) header the merge reads.
+    return (size_t)num_splits * rows * ((size_t)head_dim * 2 + sizeof(float)) + (size_t)batch * 2 * sizeof(int);
 }
 
 int decode_default_splits(int batch, int num_heads, int num_kv_heads, int seqlen_q, int capacity) {

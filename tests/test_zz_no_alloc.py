@@ -93,10 +93,10 @@ def test_noalloc_matches_the_workspace_entry_point_on_consecutive_calls():
 
 
 def test_noalloc_cuts_its_split_count_to_the_scratch():
-    """16 sequences x 16 query rows x D = 128: the library's choice (9 splits, 19 MB of partials)
-    does not fit 16 MiB; the allocation-free call runs the largest count that does (7) and equals
-    the workspace entry point at that count."""
-    batch, cap, nq, d = 16, 8192, 16, 128
+    """16 sequences x 16 query rows x D = 256: the library's choice (9 split slots per sequence,
+    19 MB of 16-bit partials) does not fit 16 MiB; the allocation-free call runs the largest count
+    that does (7) and equals the workspace entry point at that count."""
+    batch, cap, nq, d = 16, 8192, 16, 256
     g = torch.Generator().manual_seed(21)
     lens = torch.randint(0, cap - nq, (batch,), generator=g).tolist()
     q, kc, vc, kn, vn, cl = _gpu(*_inputs(batch, cap, lens, nq, 16, 4, d, 21))
@@ -118,7 +118,8 @@ def test_noalloc_cuts_its_split_count_to_the_scratch():
 
 
 def test_noalloc_rejects_an_explicit_split_count_beyond_the_scratch():
-    batch, cap, nq, d = 16, 8192, 16, 128
+    # 12 split slots of 16 sequences x 16 query rows x D = 256: 25 MB of partials > 16 MiB.
+    batch, cap, nq, d = 16, 8192, 16, 256
     q, kc, vc, kn, vn, cl = _gpu(*_inputs(batch, cap, [100] * batch, nq, 16, 4, d, 22))
     kc0 = kc.clone()
     p, out, lse = _params(q, kc, vc, cl, kn, vn, 12)
