@@ -59,11 +59,13 @@ struct BwdArgs {
     int gx, gy, gz;  // blocks per (group, sequence), sequences, groups; decoded by block_coord
     // Stored dS (the dK/dV pass writes it, the dS-driven dQ pass reads it). A pass covers the
     // query heads of KV heads kv0, kv0 + 1, ...; its r-th query head's blocks start at
-    // ds + r * ds_hs; there, query tile t (ds_tile_base + tile within its sequence, < ds_nqt)
-    // owns a row of ds_w 32 x 32 blocks, at slot = key block - the first key block it sees.
+    // ds + r * ds_hs (ds_blocks 2 KB blocks each); there, sequence b's rows start at block
+    // ds_seq_base(b) (compact rows, see ds_row_off).
     uint16_t* ds;
     int64_t ds_hs;
-    int ds_w, ds_nqt;
+    int64_t ds_blocks;
+    const int64_t* ds_base;  // packed batches: first block of each sequence (device table)
+    int64_t ds_seq_dense;    // dense batches: blocks per sequence
     int kv0;
     // Block queues of the queued (persistent) stored-dS dK/dV kernel: kQueueSet ints per pass
     // (one counter per XCD queue) at sched + pass * kQueueSet; the delta kernel zeroes
@@ -76,10 +78,102 @@ typedef __attribute__((address_space(1))) s16x8 gs16x8;
 
 // First 32-key block a 32-row query tile i sees (the tile's band starts at key 32 i + lo_f).
 __device__ inline int ds_first_block(int i, int lo_f) { return max(i + (lo_f >> 5), 0); }
-// Index of a sequence's first query tile in the dS rows: packed sequences start at
-// floor(tok0 / 32) + b, which keeps every sequence's tiles apart; dense batches at b * tiles.
-__device__ inline int ds_tile_base(int b, int64_t tok0, int seqlen_q, bool varlen) {
-    return varlen ? (int)(tok0 >> 5) + b : b * ((seqlen_q + 31) >> 5);
+
+// ---- compact stored-dS rows ------------------------------------------------------------
+//
+// Query tile i of a sequence owns one row of 2 KB dS blocks, slot = key block - the first key
+// block it sees, with exactly as many slots as its band touches: the first block is
+// clamp(i + c_lo, 0, N) and the end clamp(i + c_hi, 0, N) for a full tile, with
+// c_lo = floor(lo_f / 32), c_hi = 1 + ceil(hi_f / 32) and N the sequence's key blocks
+// (the last, partial tile touches no more). Row i therefore starts at
+//   row_off(i) = sum_{i' < i} clamp(i' + c_hi, 0, N) - sum_{i' < i} clamp(i' + c_lo, 0, N),
+// each sum in closed form, so the dK/dV writer and the dQ reader locate any row without a
+// table; a sequence's rows take row_off(tiles) blocks (a causal sequence of n tiles:
+// n (n + 1) / 2, where rows of the longest sequence's width took n * n_max). Sequences follow
+// one another: dense batch b at b * blocks(seqlen_q, seqlen_k); packed sequences at the
+// prefix sums of their own sizes, a table built on the device before the dK/dV pass
+// (ds_build_table). Query heads outermost.
+struct DsBand {
+    int c_lo, c_hi, nkb;
+};
+__host__ __device__ inline DsBand ds_band(int q_len, int k_len, int wl, int wr) {
+    const int lo_f = band_lo(k_len, q_len, wl), hi_f = band_hi(k_len, q_len, wr);
+    DsBand d;
+    d.c_lo = lo_f >> 5;               // floor(lo_f / 32)
+    d.c_hi = 1 - ((-hi_f) >> 5);      // 1 + ceil(hi_f / 32)
+    d.nkb = (k_len + 31) >> 5;
+    return d;
+}
+// sum_{i' < i} clamp(i' + c, 0, n)
+__host__ __device__ inline long long ds_clamp_sum(long long c, long long i, long long n) {
+    const long long lo = -c < 0 ? 0 : (-c > i ? i : -c);
+    const long long hi = n - c < 0 ? 0 : (n - c > i ? i : n - c);
+    return (hi - lo) * c + (hi * (hi - 1) - lo * (lo - 1)) / 2 + (i - hi) * n;
+}
+__host__ __device__ inline long long ds_row_off(const DsBand& d, int i) {
+    return ds_clamp_sum(d.c_hi, i, d.nkb) - ds_clamp_sum(d.c_lo, i, d.nkb);
+}
+// Slots of row i: row_off(i + 1) - row_off(i), for walking consecutive tiles.
+__host__ __device__ inline int ds_row_w(const DsBand& d, int i) {
+    const int hi = i + d.c_hi < 0 ? 0 : (i + d.c_hi > d.nkb ? d.nkb : i + d.c_hi);
+    const int lo = i + d.c_lo < 0 ? 0 : (i + d.c_lo > d.nkb ? d.nkb : i + d.c_lo);
+    return hi - lo;
+}
+__host__ __device__ inline long long ds_seq_blocks(int q_len, int k_len, int wl, int wr) {
+    if (q_len <= 0 || k_len <= 0) return 0;
+    return ds_row_off(ds_band(q_len, k_len, wl, wr), (q_len + 31) >> 5);
+}
+// First block of sequence b's rows within a query head's dS.
+__device__ inline int64_t ds_seq_base(const BwdArgs& a, int b) {
+    return a.cu_q != nullptr ? a.ds_base[b] : (int64_t)b * a.ds_seq_dense;
+}
+
+// The packed batch's table of sequence starts (exclusive prefix sums of ds_seq_blocks over the
+// sequences, ds_base[batch] = the total), by one block of NT threads: each thread sums a run of
+// consecutive sequences (eight length reads in flight at a time), then one block-wide scan
+// over the runs. Must complete before the dK/dV pass that stores dS (stream order).
+template <int NT>
+__device__ void ds_build_table(const BwdArgs& a, int64_t* table) {
+    __shared__ int64_t part[NT / 64];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int per = (a.batch + NT - 1) / NT;
+    const int b0 = tid * per, b1 = min(b0 + per, a.batch);
+    auto blocks = [&](int b) {
+        const int ql = a.cu_q[b + 1] - a.cu_q[b], kl = a.cu_k[b + 1] - a.cu_k[b];
+        return ds_seq_blocks(ql, kl, a.wl, a.wr);
+    };
+    int64_t run = 0;
+    for (int b = b0; b < b1; b += 8) {
+        int64_t s[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s[u] = b + u < b1 ? blocks(b + u) : 0;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) run += s[u];
+    }
+    // Block-wide exclusive scan of the runs.
+    int64_t inc = run;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int64_t y = __shfl_up(inc, off);
+        if (lane >= off) inc += y;
+    }
+    if (lane == 63) part[w] = inc;
+    __syncthreads();
+    int64_t before = 0;
+    for (int i = 0; i < w; ++i) before += part[i];
+    int64_t at = before + inc - run;
+    for (int b = b0; b < b1; b += 8) {
+        int64_t s[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s[u] = b + u < b1 ? blocks(b + u) : 0;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            if (b + u < b1) table[b + u] = at;
+            at += s[u];
+        }
+    }
+    if (b1 == a.batch && b0 < b1) table[a.batch] = at;
+    if (a.batch == 0 && tid == 0) table[0] = 0;
 }
 
 // Layout of one stored 32 x 32 dS block (bf16, 2 KB): two 1 KB halves by query half
@@ -223,8 +317,11 @@ __device__ inline const BwdArgs& fresh_args() {
     return *(const BwdArgs*)kp;
 }
 
-__global__ void sched_zero_kernel(int* p, int n) {
-    for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0;
+// The two stored-dS halves' set-up, one block of 64 threads: the block-queue counters start at
+// zero, and packed batches get their sequence-start table.
+__global__ __launch_bounds__(64) void sched_zero_kernel(BwdArgs a) {
+    for (int i = threadIdx.x; i < a.sched_zero; i += blockDim.x) a.sched[i] = 0;
+    if (a.ds_base != nullptr) ds_build_table<64>(a, const_cast<int64_t*>(a.ds_base));
 }
 
 // ---- 1. delta = rowsum(dO * O) ---------------------------------------------------------
@@ -243,9 +340,11 @@ __global__ __launch_bounds__(256) void bwd_delta_kernel(BwdArgs a) {
     const int r_lo = varlen ? a.cu_q[0] : 0;
     const int r_hi = varlen ? a.cu_q[a.batch] : a.batch * a.seqlen_q;
     const int64_t n = (int64_t)(r_hi - r_lo) * a.num_heads;
-    // The queue counters of the passes that follow start at zero.
+    // The queue counters of the passes that follow start at zero; packed batches get their
+    // dS sequence-start table (by the last block, which has the fewest items).
     if (a.sched != nullptr && blockIdx.x == 0)
         for (int i = threadIdx.x; i < a.sched_zero; i += 256) a.sched[i] = 0;
+    if (a.ds_base != nullptr && blockIdx.x == gridDim.x - 1) ds_build_table<256>(a, const_cast<int64_t*>(a.ds_base));
     const int ch = threadIdx.x % CPR;
     const int64_t stride = (int64_t)gridDim.x * IPB;
     for (int64_t base = (int64_t)blockIdx.x * IPB + threadIdx.x / CPR; base < n; base += stride * U) {
@@ -495,17 +594,19 @@ __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
         wait_vmcnt<0>();
     }
 
-    // dS: byte address of the current head's (pass-relative) first tile row of this sequence,
-    // moved on by hpw heads per head change; the lane's 16-byte chunk within a block.
+    // dS: byte address of the current head's (pass-relative) first row of this sequence, moved
+    // on by hpw heads per head change; the lane's 16-byte chunk within a block.
     uint64_t ds_ptr = 0, ds_hstep = 0;
-    int ds_w = 0, ds_rows = 0, ds_jblk = 0, ds_lob = 0;
+    int ds_jblk = 0, ds_lob = 0;
+    int64_t ds_room = 0;  // blocks of the head's dS from this sequence's first row on
+    DsBand ds_bd = {0, 0, 0};
     if constexpr (DS) {
-        const int t0 = ds_tile_base(b, qs.tok0, a.seqlen_q, a.cu_q != nullptr);
-        ds_w = sgpr_copy(a.ds_w);
-        ds_rows = sgpr_copy(a.ds_nqt) - t0;
+        const int64_t base = ds_seq_base(a, b);
+        ds_room = a.ds_blocks - base;
+        ds_bd = ds_band(q_len, k_len, a.wl, a.wr);
         ds_hstep = (uint64_t)hpw * (uint64_t)a.ds_hs * 2;
         ds_ptr = reinterpret_cast<uint64_t>(a.ds) +
-                 ((uint64_t)((int64_t)(kvh - a.kv0) * a.group + hs) * (uint64_t)a.ds_hs + (uint64_t)t0 * ds_w * 1024) * 2;
+                 ((uint64_t)((int64_t)(kvh - a.kv0) * a.group + hs) * (uint64_t)a.ds_hs + (uint64_t)base * 1024) * 2;
         ds_jblk = nw0 >> 5;
         ds_lob = lo_f >> 5;
     }
@@ -610,8 +711,9 @@ __global__ __launch_bounds__(NW * 64) void bwd_dkdv_kernel(BwdArgs a) {
             ds_keep[0] = dsb[0];
             ds_keep[1] = dsb[1];
             if (partial_block && key >= k_len) ds_keep[0] = ds_keep[1] = s16x8{0, 0, 0, 0, 0, 0, 0, 0};
-            ds_keep_ok = slot < ds_w && ti < ds_rows;
-            ds_keep_at = ds_ptr + (uint64_t)(ti * ds_w + slot) * 2048;
+            const int64_t blk = ds_row_off(ds_bd, ti) + slot;
+            ds_keep_ok = slot >= 0 && blk < ds_room;
+            ds_keep_at = ds_ptr + (uint64_t)blk * 2048;
             if (head_done) ds_ptr += ds_hstep;
         }
         // With the transposed operands already in registers the stage is free: refill it now
@@ -958,14 +1060,15 @@ __device__ __forceinline__ void dkdv_pair_block(const BwdArgs& a, int block) {
         // dS rows of this pair's first head (pass-relative) in the sequence; moved on by HPW
         // heads per head change.
         uint64_t ds_ptr = 0, ds_hstep = 0;
-        int ds_w = 0, ds_rows = 0;
+        int64_t ds_room = 0;  // blocks of the head's dS from this sequence's first row on
+        DsBand ds_bd = {0, 0, 0};
         if constexpr (DS) {
-            const int t0 = ds_tile_base(b, qs.tok0, a.seqlen_q, a.cu_q != nullptr);
-            ds_w = sgpr_copy(a.ds_w);
-            ds_rows = sgpr_copy(a.ds_nqt) - t0;
+            const int64_t base = ds_seq_base(a, b);
+            ds_room = a.ds_blocks - base;
+            ds_bd = ds_band(q_len, k_len, a.wl, a.wr);
             ds_hstep = (uint64_t)HPW * (uint64_t)a.ds_hs * 2;
             ds_ptr = reinterpret_cast<uint64_t>(a.ds) +
-                     ((uint64_t)((int64_t)(kvh - a.kv0) * a.group + hs) * (uint64_t)a.ds_hs + (uint64_t)t0 * ds_w * 1024) * 2;
+                     ((uint64_t)((int64_t)(kvh - a.kv0) * a.group + hs) * (uint64_t)a.ds_hs + (uint64_t)base * 1024) * 2;
         }
         const int ds_jblk = nw0 >> 5, ds_lob = lo_f >> 5;
         const unsigned ds_lane0 = (unsigned)(ds_chunk(0, g, l32) * 16), ds_lane1 = (unsigned)(ds_chunk(1, g, l32) * 16);
@@ -976,6 +1079,10 @@ __device__ __forceinline__ void dkdv_pair_block(const BwdArgs& a, int block) {
         s16x8 qt[DB][2];
         int pm0 = 0;
         uint64_t pds = 0;
+        // Row offset of the previous step's tile (prow) and of this step's (row_cur), walked by
+        // one row width per tile and reset to the band's first tile at each head.
+        int64_t prow = 0, row_cur = 0, row0 = 0;
+        if constexpr (DS) row_cur = row0 = ds_row_off(ds_bd, ur.lo >> 5);
         auto read_p = [&](int slot, f32x4* x) {
             const float* xp = &xbuf[slot][pair][0];
 #pragma unroll
@@ -1004,8 +1111,9 @@ __device__ __forceinline__ void dkdv_pair_block(const BwdArgs& a, int block) {
                 // keys past the sequence as 0.
                 const int ti = pm0 >> 5;
                 const int slot = ds_jblk - max(ti + ds_lob, 0);  // ds_first_block(ti, lo_f)
-                if (pm0 >= wr.lo && pm0 < wr.hi && slot >= 0 && slot < ds_w && ti < ds_rows) {
-                    const uint64_t blk = pds + (uint64_t)(ti * ds_w + slot) * 2048;
+                const int64_t bi = prow + slot;
+                if (pm0 >= wr.lo && pm0 < wr.hi && slot >= 0 && bi < ds_room) {
+                    const uint64_t blk = pds + (uint64_t)bi * 2048;
                     const s16x8 z = {0, 0, 0, 0, 0, 0, 0, 0};
                     // Non-temporal: the dQ pass reads them long after; kept out of the way
                     // of the Q / dO tiles other workgroups reuse through L2 (445 -> 434 us).
@@ -1047,6 +1155,10 @@ __device__ __forceinline__ void dkdv_pair_block(const BwdArgs& a, int block) {
             __builtin_amdgcn_sched_barrier(0);
             pm0 = m0;
             pds = ds_ptr;
+            if constexpr (DS) {
+                prow = row_cur;
+                row_cur = cur_tile + 1 == ntiles ? row0 : row_cur + ds_row_w(ds_bd, m0 >> 5);
+            }
             if (cur_tile + 1 == ntiles) ds_ptr += ds_hstep;
             cur_tile = cur_tile + 1 == ntiles ? 0 : cur_tile + 1;
             // Q^T operands of this tile's dK product (kept for the next step), issued after the
@@ -1396,7 +1508,8 @@ __device__ __forceinline__ void dq_ds_block(const BwdArgs& a, int logical) {
     }
     const int nsteps = wg_hi > wg_lo ? (wg_hi - wg_lo + BN - 1) / BN : 0;
     const int s_w = tok_base + (wave / hpw) * RQ;
-    const int ds_t0 = ds_tile_base(b, qs.tok0, a.seqlen_q, a.cu_q != nullptr);
+    const int64_t ds_base = ds_seq_base(a, b);
+    const DsBand ds_bd = ds_band(q_len, k_len, a.wl, a.wr);
     int blo[2], bhi[2];
     uint64_t ds_row[2];  // byte address of each tile's slot 0 minus its first block
 #pragma unroll
@@ -1404,17 +1517,19 @@ __device__ __forceinline__ void dq_ds_block(const BwdArgs& a, int logical) {
         const int s0 = s_w + 32 * tt;
         const int bs = q_len - s0 < 32 ? q_len - s0 : 32;
         blo[tt] = bhi[tt] = 0;
-        const int row = ds_t0 + (s0 >> 5);
-        if (bs > 0 && row < a.ds_nqt) {
+        const int i = s0 >> 5;
+        const int64_t row = ds_base + ds_row_off(ds_bd, i);
+        if (bs > 0) {
             const Ranges r = block_ranges(s0, bs, lo_f, hi_f, k_len, 32);
-            if (r.hi > r.lo) {
-                blo[tt] = ds_first_block(s0 >> 5, lo_f);  // = r.lo / 32
+            const int64_t w = ds_row_w(ds_bd, i);  // the row's slots
+            if (r.hi > r.lo && row + w <= a.ds_blocks) {
+                blo[tt] = ds_first_block(i, lo_f);  // = r.lo / 32
                 bhi[tt] = (r.hi + 31) >> 5;
-                bhi[tt] = bhi[tt] - blo[tt] > a.ds_w ? blo[tt] + a.ds_w : bhi[tt];
+                bhi[tt] = bhi[tt] - blo[tt] > w ? blo[tt] + (int)w : bhi[tt];
             }
         }
         ds_row[tt] = reinterpret_cast<uint64_t>(a.ds) +
-                     (uint64_t)(((int64_t)hrel * a.ds_hs + ((int64_t)row * a.ds_w - blo[tt]) * 1024) * 2);
+                     (uint64_t)(((int64_t)hrel * a.ds_hs + (row - blo[tt]) * 1024) * 2);
     }
 
     const uint16_t* kbase = a.k + (int64_t)b * a.kbs + ks.tok0 * a.kts + (int64_t)kvh * a.khs;
@@ -1565,7 +1680,9 @@ BwdArgs make_args(const mykfa_bwd_params& p) {
     a.batch = f.batch;
     a.ds = nullptr;
     a.ds_hs = 0;
-    a.ds_w = a.ds_nqt = 0;
+    a.ds_blocks = 0;
+    a.ds_base = nullptr;
+    a.ds_seq_dense = 0;
     a.kv0 = 0;
     a.sched = nullptr;
     a.sched_zero = 0;
@@ -1720,16 +1837,31 @@ hipError_t ds_passes(BwdArgs a, const mykfa_bwd_params& p, int kv_per_pass, hipS
     return e;
 }
 
-// Rows of the dS layout: query tiles over the whole launch (see ds_tile_base) and the slots per
-// tile (the most 32-key blocks one 32-row tile's band can touch).
-int64_t ds_tiles(const mykfa_fwd_params& f) {
-    if (f.cu_seqlens_q != nullptr) return f.lse_head_stride / 32 + f.batch + 1;
-    return (int64_t)f.batch * ((f.max_seqlen_q + 31) / 32);
-}
-int64_t ds_slots(const mykfa_fwd_params& f) {
+// Blocks per query head of the compact dS layout. Dense batches: exact. Packed batches: the
+// host knows only the packed row count T (lse_head_stride), the batch B and max_seqlen, so the
+// size is an upper bound over all length distributions: at most (T + 31 B) / 32 query tiles,
+// each with at most the widest band's slots; and for causal self-attention (cu_seqlens_q ==
+// cu_seqlens_k, right window 0) a tile's row widths grow along its sequence (1, 2, ... up to
+// the window), so a sequence's mean row width grows with its length and no batch exceeds the
+// tiles times the mean width of a max_seqlen sequence (cfg3: 337 MB per KV head where rows of
+// the longest sequence's width took 673 MB; 164 MB are written).
+int64_t ds_head_blocks(const mykfa_fwd_params& f) {
+    const int wl = f.window_left, wr = f.window_right;
+    if (f.cu_seqlens_q == nullptr) return (int64_t)f.batch * ds_seq_blocks(f.max_seqlen_q, f.max_seqlen_k, wl, wr);
+    const int64_t tiles = (f.lse_head_stride + 31LL * f.batch) / 32;
     const int64_t all = (f.max_seqlen_k + 31) / 32;
-    const int64_t band = (32 + (int64_t)f.window_left + f.window_right + 31) / 32 + 1;
-    return all < band ? all : band;
+    const int64_t band = (32 + (int64_t)wl + wr + 31) / 32 + 1;
+    const int64_t rect = tiles * (all < band ? all : band);
+    if (f.cu_seqlens_q != f.cu_seqlens_k || wr != 0) return rect;
+    const int M = f.max_seqlen_q < f.max_seqlen_k ? f.max_seqlen_q : f.max_seqlen_k;
+    const int64_t ntM = (M + 31) / 32;
+    if (ntM <= 0) return rect;
+    const int64_t tri = (tiles * ds_seq_blocks(M, M, wl, wr) + ntM - 1) / ntM;
+    return tri < rect ? tri : rect;
+}
+// Bytes of the packed batch's sequence-start table (batch + 1 int64), 256-byte granular.
+size_t ds_table_bytes(const mykfa_fwd_params& f) {
+    return f.cu_seqlens_q == nullptr ? 0 : ((size_t)(f.batch + 1) * 8 + 255) / 256 * 256;
 }
 
 }  // namespace
@@ -1741,30 +1873,38 @@ size_t bwd_ds_bytes_per_kv_head(const mykfa_bwd_params& p) {
     if (f.head_dim != 128) return 0;
     if (f.batch <= 0 || f.max_seqlen_q <= 0 || f.max_seqlen_k <= 0) return 0;
     const int64_t group = f.num_heads / f.num_kv_heads;
-    return (size_t)(group * ds_tiles(f) * ds_slots(f)) * 2048 + kSchedBytes;
+    return (size_t)(group * ds_head_blocks(f)) * 2048 + kSchedBytes + ds_table_bytes(f);
 }
 
-BwdArgs ds_args(const mykfa_bwd_params& p, void* ws) {
+// Workspace of kv_heads KV heads' worth: their dS, then their block-queue counters, then the
+// sequence-start table.
+BwdArgs ds_args(const mykfa_bwd_params& p, void* ws, int kv_heads) {
     BwdArgs a = make_args(p);
     a.ds = static_cast<uint16_t*>(ws);
-    a.ds_w = (int)ds_slots(p.fwd);
-    a.ds_nqt = (int)ds_tiles(p.fwd);
-    a.ds_hs = (int64_t)a.ds_nqt * a.ds_w * 1024;
+    a.ds_blocks = ds_head_blocks(p.fwd);
+    a.ds_hs = a.ds_blocks * 1024;
+    a.ds_seq_dense = p.fwd.cu_seqlens_q == nullptr ? ds_seq_blocks(p.fwd.max_seqlen_q, p.fwd.max_seqlen_k,
+                                                                   p.fwd.window_left, p.fwd.window_right)
+                                                   : 0;
+    char* tail = static_cast<char*>(ws) + (size_t)kv_heads * ((size_t)a.group * a.ds_hs * 2 + kSchedBytes);
+    a.ds_base = p.fwd.cu_seqlens_q != nullptr ? reinterpret_cast<const int64_t*>(tail) : nullptr;
     return a;
 }
 
 hipError_t launch_bwd_ds(const mykfa_bwd_params& p, void* ws, int kv_per_pass, hipStream_t stream) {
-    const BwdArgs a = ds_args(p, ws);
+    const BwdArgs a = ds_args(p, ws, kv_per_pass);
     if (p.fwd.dtype == MYKFA_BF16) return ds_passes<BF16>(a, p, kv_per_pass, stream);
     return ds_passes<FP16>(a, p, kv_per_pass, stream);
 }
 
 hipError_t launch_bwd_ds_half(const mykfa_bwd_params& p, void* ws, bool dq, hipStream_t stream) {
-    BwdArgs a = ds_args(p, ws);
     const int n = p.fwd.num_kv_heads;
-    // One pass over every KV head: its queue counters after the dS, zeroed here.
+    BwdArgs a = ds_args(p, ws, n);
+    // One pass over every KV head: its queue counters after the dS, zeroed here, and the
+    // sequence-start table (the same in both halves).
     a.sched = reinterpret_cast<int*>(a.ds + (int64_t)n * a.group * a.ds_hs);
-    hipLaunchKernelGGL(sched_zero_kernel, dim3(1), dim3(64), 0, stream, a.sched, kQueueSet);
+    a.sched_zero = kQueueSet;
+    hipLaunchKernelGGL(sched_zero_kernel, dim3(1), dim3(64), 0, stream, a);
     if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     const bool pair = dkdv_pair_enabled();
     if (p.fwd.dtype == MYKFA_BF16) {

@@ -419,8 +419,8 @@ __host__ __device__ inline Ranges block_ranges(int s0, int BS, int lo_off, int h
 }
 
 // Offsets of windowed causal masking: query i sees key j iff lo_off <= j - i <= hi_off.
-__device__ inline int band_lo(int k_len, int q_len, int wl) { return k_len - q_len - wl; }
-__device__ inline int band_hi(int k_len, int q_len, int wr) {
+__host__ __device__ inline int band_lo(int k_len, int q_len, int wl) { return k_len - q_len - wl; }
+__host__ __device__ inline int band_hi(int k_len, int q_len, int wr) {
     // wr may be 2^30: keep the sum within int32
     long long v = (long long)k_len - q_len + wr;
     return v > (1 << 30) ? (1 << 30) : (int)v;

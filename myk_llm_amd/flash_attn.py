@@ -66,14 +66,17 @@ def _available_bytes(device: torch.device) -> int:
 
 def _plan_ds_workspace(per_head: int, kv_heads: int, budget: int, alloc, available=None):
     """The stored-dS workspace of the backward: (KV heads per pass, buffer), or (0, None) for
-    the recomputing backward. Takes as many KV heads per pass as the budget allows (at most
-    every head); a request above _DS_CHECK_FREE_ABOVE is first capped at 80 % of
-    `available()` bytes, and an allocation that still fails (torch.OutOfMemoryError) is retried
-    with half as many heads, down to none. Both schedules give results within the same
-    tolerance of the reference, so running out of memory costs speed, never the call."""
+    the recomputing backward. Which backward runs depends on the shape alone (one KV head's
+    workspace within the budget); how many KV heads share a pass may also depend on free
+    memory, which changes no result bit (KV heads are independent). Takes as many KV heads
+    per pass as the budget allows (at most every head); a request above _DS_CHECK_FREE_ABOVE
+    is capped at 80 % of `available()` bytes, but never below one head, and an allocation that
+    still fails (torch.OutOfMemoryError) is retried with half as many heads. Only when one head's
+    workspace cannot be allocated at all does the call take the recomputing backward (results
+    within the same tolerance of the reference, not bitwise those of the stored-dS one)."""
     heads = min(kv_heads, budget // per_head) if per_head > 0 else 0
-    if heads > 0 and available is not None and heads * per_head > _DS_CHECK_FREE_ABOVE:
-        heads = min(heads, int(0.8 * available()) // per_head)
+    if heads > 1 and available is not None and heads * per_head > _DS_CHECK_FREE_ABOVE:
+        heads = max(1, min(heads, int(0.8 * available()) // per_head))
     while heads > 0:
         try:
             return heads, alloc(heads * per_head)

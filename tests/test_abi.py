@@ -235,18 +235,18 @@ def _bwd_params(head_dim, window_left=_lib.UNBOUNDED, window_right=0):
 
 
 def test_stored_ds_workspace_size(L):
-    """mykfa_bwd_workspace_per_kv_head: one 2 KB dS block per (32-row query tile, slot) for each
-    of a KV head's query heads, plus 4 KB for the block-queue counters of the queued kernels;
-    slots per tile = the most 32-key blocks one tile's band can touch. head_dim 128 only; 0 for
-    other head dims and for invalid params."""
+    """mykfa_bwd_workspace_per_kv_head: one 2 KB dS block per (32-row query tile, key block its
+    band touches) for each of a KV head's query heads (compact rows), plus 4 KB for the
+    block-queue counters of the queued kernels. head_dim 128 only; 0 for other head dims and for
+    invalid params."""
     b = _bwd_params(128)
     assert L.mykfa_validate_bwd(ctypes.byref(b)) == _lib.OK
-    tiles, group, sched = 2 * 128 // 32, 4, 4096
-    # Causal, unbounded left: a tile can touch every key block of its sequence (4 of them).
-    assert L.mykfa_bwd_workspace_per_kv_head(ctypes.byref(b)) == group * tiles * 4 * 2048 + sched
-    # A 31-key left window: a tile's band spans 63 keys, i.e. at most 3 blocks.
+    seqs, group, sched = 2, 4, 4096
+    # Causal, unbounded left, 4 tiles per sequence: rows of 1, 2, 3, 4 blocks.
+    assert L.mykfa_bwd_workspace_per_kv_head(ctypes.byref(b)) == group * seqs * 10 * 2048 + sched
+    # A 31-key left window: rows of 1, 2, 2, 2 blocks (a tile's band reaches one block back).
     b = _bwd_params(128, 31, 0)
-    assert L.mykfa_bwd_workspace_per_kv_head(ctypes.byref(b)) == group * tiles * 3 * 2048 + sched
+    assert L.mykfa_bwd_workspace_per_kv_head(ctypes.byref(b)) == group * seqs * 7 * 2048 + sched
     assert L.mykfa_bwd_workspace_per_kv_head(ctypes.byref(_bwd_params(64))) == 0
     b = _bwd_params(128)
     b.dout = 0

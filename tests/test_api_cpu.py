@@ -134,8 +134,10 @@ def test_ds_workspace_plan_caps_and_falls_back():
     assert _plan_ds_workspace(per, 4, 2 * per + 5, alloc) == (2, 2 * per)
     assert _plan_ds_workspace(0, 4, 4 << 30, alloc) == (0, None)
     assert _plan_ds_workspace(per, 4, per - 1, alloc) == (0, None)
-    # Available memory caps a large request at 80 %.
+    # Available memory caps a large request at 80 %, but never below one head: the choice of
+    # backward depends on the shape only.
     assert _plan_ds_workspace(per, 4, 4 << 30, alloc, lambda: 3 * per)[0] == 2
+    assert _plan_ds_workspace(per, 4, 4 << 30, alloc, lambda: 0)[0] == 1
     # Small requests skip the query.
     small = _DS_CHECK_FREE_ABOVE // 4
     assert _plan_ds_workspace(small, 4, 4 << 30, alloc, lambda: 0)[0] == 4
