@@ -687,6 +687,8 @@ def main():
                     help="only the fused linear + cross-entropy at the reference model's head (for profiling)")
     ap.add_argument("--block-io-only", action="store_true",
                     help="only the attention-block prologue / epilogue kernels at the cfg3 shape (for profiling)")
+    ap.add_argument("--reference-shapes-only", action="store_true",
+                    help="only the reference benchmark's six shapes, eager fwd and fwd+bwd (for profiling)")
     ap.add_argument("--graph", action="store_true", help="time prefill steps as HIP graph replays instead of eager calls")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run a plain 256 MiB fp32 copy kernel 3 times (reads and writes 2^28 bytes "
@@ -727,6 +729,9 @@ def main():
         return
     if args.block_io_only:
         print(json.dumps({"block_io_cfg3": measure_block_io(W["cfg3"], args.steps)}), flush=True)
+        return
+    if args.reference_shapes_only:
+        print(json.dumps({"reference_shapes": measure_reference_shapes(max(10, min(args.steps, 30)))}), flush=True)
         return
     w = W[args.workload]
     log(f"headline {w.name}: fwd+bwd, steps={args.steps} warmup={args.warmup}")

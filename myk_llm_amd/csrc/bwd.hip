@@ -1791,7 +1791,10 @@ hipError_t dq_dtype(const BwdArgs& a, int D, hipStream_t s) {
     switch (D) {
         case 16: return dq_launch<16, 64, 4, 4, T>(a, s);
         case 32: return dq_launch<32, 64, 4, 4, T>(a, s);
-        case 64: return dq_launch<64, 32, 4, 4, T>(a, s);
+        // 64-key steps in 2 stages: half the steps (barriers, ring waits) of 32-key steps on the
+        // longest causal rows; cfg2 dQ 51.9 -> 49.9 us (32 keys in 3, 4 or 6 stages and 64
+        // keys in 3 stages measured slower).
+        case 64: return dq_launch<64, 64, 4, 2, T>(a, s);
         case 128: return dq_launch<128, 64, 4, 2, T>(a, s);
         case 256: return dq_launch<256, 32, 4, 3, T>(a, s);
         default: return hipErrorInvalidValue;
