@@ -122,7 +122,10 @@ typedef struct mykfa_bwd_params {
  */
 typedef struct mykfa_decode_params {
     mykfa_fwd_params fwd;   /* cu_seqlens_* must be NULL; seqused_k NULL = max_seqlen_k keys */
-    int32_t num_splits;     /* 0 = choose (mykfa_decode_num_splits) */
+    int32_t num_splits;     /* partial slots per sequence on average (the workspace's segment
+                             * pool is num_splits * batch); the kernel splits each sequence by
+                             * its actual length within that pool. 1 = one split per sequence,
+                             * no merge; 0 = choose (mykfa_decode_num_splits) */
     int32_t seqlen_new;     /* new keys per sequence after seqused_k[b] (0 = none) */
     const void* k_new;      /* (batch, seqlen_new, Hkv, D) or NULL */
     const void* v_new;
@@ -331,10 +334,14 @@ int mykfa_bwd(const mykfa_bwd_params* p, mykfa_stream_t stream);
  * then dQ = scale * dS K from those blocks: five products per (query tile, key block) pair
  * instead of seven. Deterministic: no sum depends on the order of workgroups (dK/dV takes its
  * blocks from queues through atomic counters, which decide only which workgroup computes a
- * block). The workspace holds the dS of whole KV heads and the queue counters:
- * mykfa_bwd_workspace_per_kv_head bytes each (0 when head_dim is not 128, where the trade does
- * not pay); with workspace_bytes >= n times that, KV heads are processed in passes of up to n.
- * With less than one KV head's worth this is mykfa_bwd (dQ recomputes S and dP). */
+ * block). The workspace holds the dS of whole KV heads (each query tile's row holds exactly
+ * the key blocks its band touches), the queue counters and, for packed batches, a table of
+ * sequence starts built on the device: mykfa_bwd_workspace_per_kv_head bytes per KV head (0 when
+ * head_dim is not 128, where the trade does not pay; for packed batches an upper bound over all
+ * length distributions with the given rows, batch and max_seqlen); with workspace_bytes >= n
+ * times that, KV heads are processed in passes of up to n, with identical results for every n.
+ * With less than one KV head's worth this is mykfa_bwd (dQ recomputes S and dP). The workspace
+ * must be 16-byte aligned (MYKFA_ERR_INVALID otherwise); its contents on entry do not matter. */
 size_t mykfa_bwd_workspace_per_kv_head(const mykfa_bwd_params* p);
 int mykfa_bwd_ws(const mykfa_bwd_params* p, void* workspace, size_t workspace_bytes, mykfa_stream_t stream);
 /* The two halves of mykfa_bwd_ws over every KV head in one launch each (workspace of
@@ -346,9 +353,11 @@ int mykfa_bwd_dkdv_ws(const mykfa_bwd_params* p, void* workspace, size_t workspa
 int mykfa_bwd_dq_ws(const mykfa_bwd_params* p, void* workspace, size_t workspace_bytes, mykfa_stream_t stream);
 
 /* ---- KV-cache decode (split-K) ------------------------------------------------------ */
-/* Split count the library would pick for this shape (>= 1): about 1400 keys per split, enough
- * workgroups to fill the chip (the query rows per KV head set how many workgroups a split
- * has), at least 128 keys per split, never a multiple of the 8 XCDs. */
+/* Slots per sequence the library would pick for this shape (>= 1): about 1400 keys of capacity
+ * per slot, enough to fill the chip (the query rows per KV head set how many workgroups a split
+ * has), at least 128 keys per slot. The split-K pass itself sizes its splits from the actual
+ * lengths on the device (so that its active workgroups fit one resident round of the chip) and
+ * uses at most num_splits * batch segments. */
 int mykfa_decode_num_splits(int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t seqlen_q,
                             int32_t capacity);
 /* Bytes of workspace mykfa_decode needs for this shape and split count. */

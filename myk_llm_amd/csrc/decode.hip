@@ -672,14 +672,14 @@ size_t decode_workspace_bytes(int batch, int num_heads, int seqlen_q, int head_d
 }
 
 int decode_default_splits(int batch, int num_heads, int num_kv_heads, int seqlen_q, int capacity) {
-    // About 1400 keys per split: each split costs a workgroup prologue and an fp32 partial row
-    // per query row that the merge reads back, and longer splits stream longer runs of the cache.
-    // Measured on the 64 x 16K-cache batch, split-K + merge: 84.8 us at 12 splits (1366 keys)
-    // against 86.3 at 46 (352 keys) for one query, 91.2 at 12 for the 4-query draft. Then at
-    // least ~512 workgroups (each kWaves KV-head units of one sequence) for short batches, at
-    // least 128 keys per split, and never a multiple of the 8 XCDs: the workgroups of split s of
-    // every sequence would then all run on one XCD, idling the XCDs of the late splits
-    // (measured: 8, 16, 32 or 64 splits 20-40 % slower than their neighbours).
+    // The slot pool (num_splits x batch segments): about 1400 keys of capacity per slot, since
+    // each split costs a workgroup prologue and a partial row per query row that the merge reads
+    // back, and longer splits stream longer runs of the cache (64 x 16K-cache batch, split-K +
+    // merge with one split count for every sequence: 84.8 us at 12 splits of 1366 keys against
+    // 86.3 at 46 of 352). Then at least ~512 workgroups (each kWaves KV-head units of one
+    // sequence) for short batches and at least 128 keys per slot. The odd count avoids a multiple
+    // of the 8 XCDs, which mattered when split s of every sequence sat at a fixed stride of the
+    // grid; the device plan now sizes the splits from the actual lengths within this pool.
     const long long kvh = num_kv_heads > 0 ? num_kv_heads : 1;
     const long long group = num_heads > 0 ? (num_heads + kvh - 1) / kvh : 1;
     const long long rows = group * (seqlen_q > 0 ? seqlen_q : 1);
