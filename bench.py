@@ -387,63 +387,87 @@ def measure_block_io(w, steps: int):
     """The attention block's prologue (q/k RMSNorm + RoPE on the fused projection, forward and
     backward with the value-gradient copy) and epilogue (output gate, forward and backward) at
     workload w's shape (positions restart at every document), as direct C-ABI launches on
-    prepared buffers. Algorithmic bytes: every tensor element read or written once, plus each
+    prepared buffers (two sets, alternated). Algorithmic bytes: every tensor element read or written once, plus each
     distinct cos/sin table row once. Beside them, the reference's composed PyTorch chain
     (mixers.py:85-89, :116-117 under autocast: separate elementwise kernels) on the same GPU."""
     from myk_llm_amd import block_io as bio
 
     t, hq, hkv, d = sum(w.lengths), w.heads, w.kv_heads, w.head_dim
-    g = torch.Generator(device="cuda").manual_seed(1)
-    qkv = torch.randn(t, (hq + 2 * hkv) * d, device="cuda", generator=g).to(torch.bfloat16)
     pos = torch.cat([torch.arange(n, device="cuda") for n in w.lengths])
     table_rows = max(w.lengths)
     cos, sin = bio.rope_tables(d, table_rows, 500000.0, device="cuda")
-    qw = 1 + 0.1 * torch.randn(d, device="cuda", generator=g)
-    kw = 1 + 0.1 * torch.randn(d, device="cuda", generator=g)
-    dq = torch.randn(t, hq, d, device="cuda", generator=g).to(torch.bfloat16)
-    dk = torch.randn(t, hkv, d, device="cuda", generator=g).to(torch.bfloat16)
-    dv = torch.randn(t, hkv, d, device="cuda", generator=g).to(torch.bfloat16)
     L = _lib.lib()
     stream = torch.cuda.current_stream().cuda_stream
-    x = qkv.unsqueeze(0)
-    q_in = x[..., :hq * d].view(1, t, hq, d)
-    k_in = x[..., hq * d:(hq + hkv) * d].view(1, t, hkv, d)
-    q_out, k_out = torch.empty_like(q_in, memory_format=torch.contiguous_format), torch.empty(1, t, hkv, d, dtype=qkv.dtype, device="cuda")
     pos2 = pos.unsqueeze(0)
-    fp = bio._prologue_params(q_in, k_in, q_out, k_out, pos2, cos, sin, qw, kw, 1e-6)
-    dqkv = torch.empty_like(x)
-    bp = _lib.QkPrologueBwdParams()
-    bp.fwd = fp
-    dq4, dk4, dv4 = dq.unsqueeze(0), dk.unsqueeze(0), dv.unsqueeze(0)
-    dq_in = dqkv[..., :hq * d].view(1, t, hq, d)
-    dk_in = dqkv[..., hq * d:(hq + hkv) * d].view(1, t, hkv, d)
-    dv_dst = dqkv[..., (hq + hkv) * d:].view(1, t, hkv, d)
-    bp.dq_out, bp.dk_out, bp.dq_in, bp.dk_in = dq4.data_ptr(), dk4.data_ptr(), dq_in.data_ptr(), dk_in.data_ptr()
-    bp.dqo_batch_stride, bp.dqo_token_stride, bp.dqo_head_stride = bio._strides3(dq4)
-    bp.dko_batch_stride, bp.dko_token_stride, bp.dko_head_stride = bio._strides3(dk4)
-    bp.dqi_batch_stride, bp.dqi_token_stride, bp.dqi_head_stride = bio._strides3(dq_in)
-    bp.dki_batch_stride, bp.dki_token_stride, bp.dki_head_stride = bio._strides3(dk_in)
-    bp.dv_src, bp.dv_dst = dv4.data_ptr(), dv_dst.data_ptr()
-    bp.dvs_batch_stride, bp.dvs_token_stride, bp.dvs_head_stride = bio._strides3(dv4)
-    bp.dvd_batch_stride, bp.dvd_token_stride, bp.dvd_head_stride = bio._strides3(dv_dst)
-    dqw, dkw = torch.empty(d, device="cuda"), torch.empty(d, device="cuda")
-    bp.dq_weight, bp.dk_weight = dqw.data_ptr(), dkw.data_ptr()
-    nws = L.mykfa_qk_prologue_bwd_workspace_size(1, t, hq, hkv, d)
-    ws = torch.empty(nws, dtype=torch.uint8, device="cuda")
-
     width = hq * d
-    og = torch.randn(t, width, device="cuda", generator=g).to(torch.bfloat16)
-    gg = torch.randn(t, width, device="cuda", generator=g).to(torch.bfloat16)
-    dy = torch.randn(t, width, device="cuda", generator=g).to(torch.bfloat16)
-    y, dx, dg = torch.empty_like(og), torch.empty_like(og), torch.empty_like(og)
-    gp = bio._gate_params(og, gg, y, dy, dx, dg)
+
+    def make_set(seed):
+        """Every buffer of the four kernels, and their parameter blocks."""
+        g = torch.Generator(device="cuda").manual_seed(seed)
+        bs = {}
+        qkv = torch.randn(t, (hq + 2 * hkv) * d, device="cuda", generator=g).to(torch.bfloat16)
+        bs["qw"] = 1 + 0.1 * torch.randn(d, device="cuda", generator=g)
+        bs["kw"] = 1 + 0.1 * torch.randn(d, device="cuda", generator=g)
+        dq = torch.randn(t, hq, d, device="cuda", generator=g).to(torch.bfloat16)
+        dk = torch.randn(t, hkv, d, device="cuda", generator=g).to(torch.bfloat16)
+        dv = torch.randn(t, hkv, d, device="cuda", generator=g).to(torch.bfloat16)
+        x = qkv.unsqueeze(0)
+        q_in = x[..., :hq * d].view(1, t, hq, d)
+        k_in = x[..., hq * d:(hq + hkv) * d].view(1, t, hkv, d)
+        q_out = torch.empty_like(q_in, memory_format=torch.contiguous_format)
+        k_out = torch.empty(1, t, hkv, d, dtype=qkv.dtype, device="cuda")
+        fp = bio._prologue_params(q_in, k_in, q_out, k_out, pos2, cos, sin, bs["qw"], bs["kw"], 1e-6)
+        dqkv = torch.empty_like(x)
+        bp = _lib.QkPrologueBwdParams()
+        bp.fwd = fp
+        dq4, dk4, dv4 = dq.unsqueeze(0), dk.unsqueeze(0), dv.unsqueeze(0)
+        dq_in = dqkv[..., :hq * d].view(1, t, hq, d)
+        dk_in = dqkv[..., hq * d:(hq + hkv) * d].view(1, t, hkv, d)
+        dv_dst = dqkv[..., (hq + hkv) * d:].view(1, t, hkv, d)
+        bp.dq_out, bp.dk_out, bp.dq_in, bp.dk_in = dq4.data_ptr(), dk4.data_ptr(), dq_in.data_ptr(), dk_in.data_ptr()
+        bp.dqo_batch_stride, bp.dqo_token_stride, bp.dqo_head_stride = bio._strides3(dq4)
+        bp.dko_batch_stride, bp.dko_token_stride, bp.dko_head_stride = bio._strides3(dk4)
+        bp.dqi_batch_stride, bp.dqi_token_stride, bp.dqi_head_stride = bio._strides3(dq_in)
+        bp.dki_batch_stride, bp.dki_token_stride, bp.dki_head_stride = bio._strides3(dk_in)
+        bp.dv_src, bp.dv_dst = dv4.data_ptr(), dv_dst.data_ptr()
+        bp.dvs_batch_stride, bp.dvs_token_stride, bp.dvs_head_stride = bio._strides3(dv4)
+        bp.dvd_batch_stride, bp.dvd_token_stride, bp.dvd_head_stride = bio._strides3(dv_dst)
+        dqw, dkw = torch.empty(d, device="cuda"), torch.empty(d, device="cuda")
+        bp.dq_weight, bp.dk_weight = dqw.data_ptr(), dkw.data_ptr()
+        nws = L.mykfa_qk_prologue_bwd_workspace_size(1, t, hq, hkv, d)
+        ws = torch.empty(nws, dtype=torch.uint8, device="cuda")
+        og = torch.randn(t, width, device="cuda", generator=g).to(torch.bfloat16)
+        gg = torch.randn(t, width, device="cuda", generator=g).to(torch.bfloat16)
+        dy = torch.randn(t, width, device="cuda", generator=g).to(torch.bfloat16)
+        y, dx, dg = torch.empty_like(og), torch.empty_like(og), torch.empty_like(og)
+        gp = bio._gate_params(og, gg, y, dy, dx, dg)
+        bs.update(x=x, q_out=q_out, k_out=k_out, dqkv=dqkv, dq4=dq4, dk4=dk4, dv4=dv4, dqw=dqw, dkw=dkw,
+                  ws=ws, og=og, gg=gg, dy=dy, y=y, dx=dx, dg=dg, fp=fp, bp=bp, gp=gp, nws=nws)
+        return bs
+
+    # Two sets of buffers, alternated call by call: a call touches 168 MB (prologue forward),
+    # 285 MB (its backward), 201 MB (gate forward) or 335 MB (gate backward) of one set, so the
+    # two sets together exceed the 256 MB Infinity Cache and every call reads its inputs from
+    # HBM, as the decode timing does.
+    sets = [make_set(1), make_set(11)]
+    turn = [0]
+
+    def alternating(launch):
+        def f():
+            launch(sets[turn[0] % 2])
+            turn[0] += 1
+        return f
 
     calls = {
-        "prologue_fwd": lambda: _lib.check(L.mykfa_qk_prologue_fwd(ctypes.byref(fp), stream)),
-        "prologue_bwd": lambda: _lib.check(L.mykfa_qk_prologue_bwd(ctypes.byref(bp), ws.data_ptr(), nws, stream)),
-        "gate_fwd": lambda: _lib.check(L.mykfa_gate_fwd(ctypes.byref(gp), stream)),
-        "gate_bwd": lambda: _lib.check(L.mykfa_gate_bwd(ctypes.byref(gp), stream)),
+        "prologue_fwd": alternating(lambda b: _lib.check(L.mykfa_qk_prologue_fwd(ctypes.byref(b["fp"]), stream))),
+        "prologue_bwd": alternating(lambda b: _lib.check(
+            L.mykfa_qk_prologue_bwd(ctypes.byref(b["bp"]), b["ws"].data_ptr(), b["nws"], stream))),
+        "gate_fwd": alternating(lambda b: _lib.check(L.mykfa_gate_fwd(ctypes.byref(b["gp"]), stream))),
+        "gate_bwd": alternating(lambda b: _lib.check(L.mykfa_gate_bwd(ctypes.byref(b["gp"]), stream))),
     }
+    s0 = sets[0]
+    x, qw, kw, dq4, dk4, dv4 = s0["x"], s0["qw"], s0["kw"], s0["dq4"], s0["dk4"], s0["dv4"]
+    og, gg, dy = s0["og"], s0["gg"], s0["dy"]
     e = 2  # bytes per element
     qk = t * (hq + hkv) * d * e
     tables = 2 * table_rows * d * 4

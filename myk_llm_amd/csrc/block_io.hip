@@ -9,7 +9,9 @@
 //                           (mixers.py:116-117).
 // All of them are HBM-bound streams: 16-byte accesses along head_dim, one row of D elements
 // per D/8 consecutive lanes, row reductions (sum of squares, the norm's dot product) by lane
-// shuffles inside those lanes.
+// shuffles inside those lanes. Every tensor element is read once, with the non-temporal hint
+// (measured with inputs coming from HBM, at cfg3's shape: prologue forward 41.2 -> 33.8 us,
+// backward 70.0 -> 60.4, gate forward 39.8 -> 38.9, gate backward 62.5 -> 54.9).
 #include "common.h"
 #include "kernels.h"
 
@@ -118,7 +120,7 @@ __global__ __launch_bounds__(kThreads) void qk_prologue_fwd_kernel(mykfa_qk_prol
                                                         p.qi_head_stride, b, s, h, c)
                                           : head_row<T>(p.k_in, p.ki_batch_stride, p.ki_token_stride,
                                                         p.ki_head_stride, b, s, h - p.num_heads, c);
-                unpack8<T>(ld16(src), x[u]);
+                unpack8<T>(ld16_stream(src), x[u]);
             }
 #pragma unroll
             for (int u = 0; u < HC; ++u) {
@@ -196,13 +198,13 @@ __global__ __launch_bounds__(kThreads) void qk_prologue_bwd_kernel(mykfa_qk_prol
                                                          p.dqo_head_stride, b, s, h, c)
                                            : head_row<T>(p.dk_out, p.dko_batch_stride, p.dko_token_stride,
                                                          p.dko_head_stride, b, s, h - f.num_heads, c);
-                unpack8<T>(ld16(gsrc), g[u]);
+                unpack8<T>(ld16_stream(gsrc), g[u]);
                 if (norm) {
                     const uint16_t* xsrc = isq ? head_row<T>(f.q_in, f.qi_batch_stride, f.qi_token_stride,
                                                              f.qi_head_stride, b, s, h, c)
                                                : head_row<T>(f.k_in, f.ki_batch_stride, f.ki_token_stride,
                                                              f.ki_head_stride, b, s, h - f.num_heads, c);
-                    unpack8<T>(ld16(xsrc), x[u]);
+                    unpack8<T>(ld16_stream(xsrc), x[u]);
                 }
             }
 #pragma unroll
@@ -272,7 +274,7 @@ __global__ __launch_bounds__(kThreads) void qk_prologue_bwd_kernel(mykfa_qk_prol
                 src[u] = head_row<T>(p.dv_src, p.dvs_batch_stride, p.dvs_token_stride, p.dvs_head_stride, b, sq, hh, cc);
                 dst[u] = const_cast<uint16_t*>(
                     head_row<T>(p.dv_dst, p.dvd_batch_stride, p.dvd_token_stride, p.dvd_head_stride, b, sq, hh, cc));
-                v[u] = ld16(src[u]);
+                v[u] = ld16_stream(src[u]);
             }
 #pragma unroll
             for (int u = 0; u < 4; ++u)
@@ -347,8 +349,8 @@ __global__ __launch_bounds__(kThreads) void gate_fwd_kernel(mykfa_gate_params p)
             if (i >= total) i = total - 1;  // in-bounds reread; the store below is skipped
             r[u] = i / cpr;
             c[u] = (int)(i - r[u] * cpr) * 8;
-            unpack8<T>(ld16(static_cast<const uint16_t*>(p.x) + r[u] * p.x_row_stride + c[u]), x[u]);
-            unpack8<T>(ld16(static_cast<const uint16_t*>(p.gate) + r[u] * p.gate_row_stride + c[u]), g[u]);
+            unpack8<T>(ld16_stream(static_cast<const uint16_t*>(p.x) + r[u] * p.x_row_stride + c[u]), x[u]);
+            unpack8<T>(ld16_stream(static_cast<const uint16_t*>(p.gate) + r[u] * p.gate_row_stride + c[u]), g[u]);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -375,9 +377,9 @@ __global__ __launch_bounds__(kThreads) void gate_bwd_kernel(mykfa_gate_params p)
             if (i >= total) i = total - 1;
             r[u] = i / cpr;
             c[u] = (int)(i - r[u] * cpr) * 8;
-            unpack8<T>(ld16(static_cast<const uint16_t*>(p.x) + r[u] * p.x_row_stride + c[u]), x[u]);
-            unpack8<T>(ld16(static_cast<const uint16_t*>(p.gate) + r[u] * p.gate_row_stride + c[u]), g[u]);
-            unpack8<T>(ld16(static_cast<const uint16_t*>(p.dy) + r[u] * p.dy_row_stride + c[u]), dy[u]);
+            unpack8<T>(ld16_stream(static_cast<const uint16_t*>(p.x) + r[u] * p.x_row_stride + c[u]), x[u]);
+            unpack8<T>(ld16_stream(static_cast<const uint16_t*>(p.gate) + r[u] * p.gate_row_stride + c[u]), g[u]);
+            unpack8<T>(ld16_stream(static_cast<const uint16_t*>(p.dy) + r[u] * p.dy_row_stride + c[u]), dy[u]);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {

@@ -124,6 +124,10 @@ __device__ inline int64_t sgpr_copy(int64_t x) {
 
 // 16-byte and 8-byte global accesses.
 __device__ inline s16x8 ld16(const uint16_t* p) { return *reinterpret_cast<const s16x8*>(p); }
+// The same with the non-temporal (streaming) hint, for tensors a kernel reads exactly once.
+__device__ inline s16x8 ld16_stream(const uint16_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const s16x8*>(p));
+}
 __device__ inline void st16(uint16_t* p, s16x8 v) { *reinterpret_cast<s16x8*>(p) = v; }
 
 // ds_read_b64_tr_b16: within each group of 16 lanes, lane j receives, for i = 0..3, element
