@@ -305,10 +305,13 @@ def _backward_launch(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, max_se
     with _DeviceGuard(dev):
         # dK/dV store dS and dQ is formed from it (five products per block pair instead of
         # seven) when at least one KV head's dS fits the budget; KV heads then go in passes.
+        # Under graph capture the free-memory query is skipped (the budget alone sizes the
+        # passes; the graph's memory pool serves the allocation).
         per_head = L.mykfa_bwd_workspace_per_kv_head(ctypes.byref(p))
+        available = None if torch.cuda.is_current_stream_capturing() else (lambda: _available_bytes(dev))
         heads, ws = (_plan_ds_workspace(per_head, k.shape[-2], _ds_budget_bytes(),
                                         lambda n: torch.empty(n, dtype=torch.uint8, device=dev),
-                                        lambda: _available_bytes(dev)) if per_head else (0, None))
+                                        available) if per_head else (0, None))
         if heads > 0:
             _lib.check(L.mykfa_bwd_ws(ctypes.byref(p), ws.data_ptr(), ws.numel(), _stream(dev)))
         else:

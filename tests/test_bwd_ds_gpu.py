@@ -249,3 +249,44 @@ def test_many_documents_either_side_of_the_queue_capacity(docs):
     assert torch.equal(dv, g_ref[2])
     torch.testing.assert_close(dk.float(), g_ref[1].float(), rtol=1e-2, atol=1e-2)
     torch.testing.assert_close(dq.float(), g_ref[0].float(), rtol=2e-2, atol=2e-2)
+
+
+def test_fwd_bwd_replays_from_a_graph(monkeypatch):
+    """Forward + backward through autograd, captured in a HIP graph on the stored-dS path (with
+    the free-memory check forced on: capture skips the query), replays bit for bit the eager
+    step, with eager work and synchronizations between the replays."""
+    _say("stored-dS backward: fwd + bwd captured in a graph")
+    monkeypatch.setattr(fa, "_DS_CHECK_FREE_ABOVE", 0)
+    torch.manual_seed(5)
+    lens = [70, 200, 33]
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0)), dtype=torch.int32).cuda()
+    q = torch.randn(sum(lens), 4, 128).to(torch.bfloat16).cuda().requires_grad_()
+    k = torch.randn(sum(lens), 2, 128).to(torch.bfloat16).cuda().requires_grad_()
+    v = torch.randn(sum(lens), 2, 128).to(torch.bfloat16).cuda().requires_grad_()
+    do = torch.randn(sum(lens), 4, 128).to(torch.bfloat16).cuda()
+
+    def step():
+        out = flash_attn_varlen_func(q, k, v, cu, cu, 200, 200, causal=True)
+        return (out.detach(),) + torch.autograd.grad(out, (q, k, v), do)
+
+    ref = step()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = step()
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        for got, want in zip(outs, ref):
+            assert torch.equal(got, want)
+        again = step()
+        torch.cuda.synchronize()
+        for got, want in zip(again, ref):
+            assert torch.equal(got, want)
