@@ -290,3 +290,42 @@ def test_fwd_bwd_replays_from_a_graph(monkeypatch):
         torch.cuda.synchronize()
         for got, want in zip(again, ref):
             assert torch.equal(got, want)
+
+
+def test_long_document_in_passes(monkeypatch):
+    """One 24576-token causal document (GQA 4, D = 128): a KV head's dS takes 2.4 GB, so the
+    default 4 GiB budget runs the stored-dS backward one KV head per pass (four passes). Against
+    the recomputing backward on the same inputs: dV bit for bit, dK and dQ to bf16 rounding, and
+    no unwritten row."""
+    _say("stored-dS backward: 24576-token document in four passes")
+    n = 24576
+    g = torch.Generator().manual_seed(12)
+    q = torch.randn(n, 16, 128, generator=g).to(torch.bfloat16).cuda().requires_grad_()
+    k = torch.randn(n, 4, 128, generator=g).to(torch.bfloat16).cuda().requires_grad_()
+    v = torch.randn(n, 4, 128, generator=g).to(torch.bfloat16).cuda().requires_grad_()
+    do = torch.randn(n, 16, 128, generator=g).to(torch.bfloat16).cuda()
+    cu = torch.tensor([0, n], dtype=torch.int32).cuda()
+    plans = []
+    real_plan = fa._plan_ds_workspace
+
+    def spy(per_head, kv_heads, budget, alloc, available=None):
+        r = real_plan(per_head, kv_heads, budget, alloc, available)
+        plans.append((per_head, r[0]))
+        return r
+
+    monkeypatch.setattr(fa, "_plan_ds_workspace", spy)
+    grads = {}
+    for mb in ("4096", "0"):
+        monkeypatch.setenv("MYKFA_BWD_DS_MAX_MB", mb)
+        out = flash_attn_varlen_func(q, k, v, cu, cu, n, n, causal=True)
+        grads[mb] = torch.autograd.grad(out, (q, k, v), do)
+        torch.cuda.synchronize()
+    per_head, heads = plans[0]
+    assert 2 << 30 < per_head < 4 << 30 and heads == 1, plans
+    assert plans[1][1] == 0
+    (dq, dk, dv), (dq0, dk0, dv0) = grads["4096"], grads["0"]
+    for x in (dq, dk, dv):
+        assert not torch.isnan(x).any()
+    assert torch.equal(dv, dv0)
+    torch.testing.assert_close(dk.float(), dk0.float(), rtol=1e-2, atol=1e-2)
+    torch.testing.assert_close(dq.float(), dq0.float(), rtol=2e-2, atol=2e-2)
