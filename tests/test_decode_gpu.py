@@ -65,6 +65,27 @@ def test_decode_head_dims(d, dtype):
     assert_lse(lse, exp_lse)
 
 
+@pytest.mark.parametrize("batch, heads, kv_heads, nq", [(300, 16, 4, 1), (300, 16, 4, 4), (9, 3, 1, 1), (9, 6, 2, 3)])
+def test_decode_large_batches_and_row_counts(batch, heads, kv_heads, nq):
+    """More sequences than the split plan's 256 threads take in one pass (every workgroup
+    computes the plan in two passes over the lengths), and sequences whose rows (query heads x
+    queries) are not a multiple of four, which the merge takes one row per wave instead of four."""
+    _say(f"decode batch={batch} H={heads}/{kv_heads} nq={nq}")
+    g = torch.Generator().manual_seed(batch + heads + nq)
+    lens = torch.randint(0, 300, (batch,), generator=g).tolist()
+    lens[0], lens[-1] = 0, 299
+    q, kc, vc, kn, vn, cl = _make(batch, 320, lens, nq, heads, kv_heads, 64, seed=batch + nq)
+    exp, exp_lse, ekc, evc = kvcache_reference(q.float(), kc.float(), vc.float(), kn.float(), vn.float(), cl, True,
+                                               (-1, -1))
+    kcg, vcg = kc.cuda(), vc.cuda()
+    out, lse = flash_attn_with_kvcache(q.cuda(), kcg, vcg, kn.cuda(), vn.cuda(), cache_seqlens=cl.cuda(),
+                                       causal=True, return_softmax_lse=True)
+    torch.cuda.synchronize()
+    assert torch.equal(kcg.cpu().float(), ekc) and torch.equal(vcg.cpu().float(), evc)
+    assert_close(out, exp)
+    assert_lse(lse, exp_lse)
+
+
 @pytest.mark.parametrize("splits", [1, 2, 3, 7, 16, 64, 128])
 def test_every_split_count_agrees(splits):
     """The C ABI with an explicit split count: split-K + merge is independent of the split.
